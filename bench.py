@@ -1,0 +1,378 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+Default workload (the headline metric): paged decode at the GQA
+Qwen2.5-7B shape - 128 sequences, 28 query / 4 kv heads, head_dim 128,
+block 16, bf16, context lengths uniform in [256, 8192] (seeded per
+sequence), pool sized to the tokens + 10 %, blocks scattered at random.
+A step is one decode pass over the batch (split-K partials + LSE merge).
+Inputs are resident in HBM before the timed region.
+
+Prints one JSON line (stdout) with the whole-job throughput in GB/s of
+algorithmic bytes (K/V read once per kv head + q + out + block tables),
+tokens/s, a roofline entry for the dominant kernel timed with HIP events on
+its own stream, and the CPU baseline: this repository's restatement of the
+reference CpuAttentionBackend (the oracle) timed on the host cores over the
+same sequences.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+METRIC = "decode-attn HBM GB/s (% of ~8 TB/s peak) + tokens/sec at GQA-7B shape, 1 GPU"
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16/fp16 MFMA
+
+DECODE_CONFIGS = {
+    # name: (num_seqs, hq, hkv, head_dim, dtype, context spec, value scale, seed, partition)
+    "opt125m": dict(num_seqs=8, hq=12, hkv=12, d=64, dtype="float32", ctx=("fixed", 128),
+                    vscale=1.0, seed=1001, partition=None,
+                    workload="paged decode, OPT-125m shape: 8 seqs, 12 heads, head_dim 64, "
+                             "block 16, fp32, context 128"),
+    "llama7b": dict(num_seqs=64, hq=32, hkv=32, d=128, dtype="float16", ctx=("fixed", 2048),
+                    vscale=0.5, seed=1002, partition=None,
+                    workload="paged decode, MHA Llama-7B shape: 64 seqs, 32 heads, head_dim 128, "
+                             "block 16, fp16, context 2048"),
+    "qwen7b": dict(num_seqs=128, hq=28, hkv=4, d=128, dtype="bfloat16", ctx=("uniform", 256, 8192),
+                   vscale=1.0, seed=1003, partition=None,
+                   workload="paged decode, GQA Qwen2.5-7B shape: 128 seqs, 28 q / 4 kv heads, "
+                            "head_dim 128, block 16, bf16, context U[256,8192] seeded per sequence"),
+    "long32k": dict(num_seqs=16, hq=32, hkv=8, d=128, dtype="float16", ctx=("fixed", 32768),
+                    vscale=1.0, seed=1004, partition=512,
+                    workload="split-K paged decode: 16 seqs, 32 q / 8 kv heads, head_dim 128, "
+                             "block 16, fp16, context 32768, partition 512"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def context_lengths(cfg) -> list[int]:
+    import torch
+
+    kind = cfg["ctx"][0]
+    if kind == "fixed":
+        return [cfg["ctx"][1]] * cfg["num_seqs"]
+    lo, hi = cfg["ctx"][1], cfg["ctx"][2]
+    return [int(torch.randint(lo, hi + 1, (1,),
+                              generator=torch.Generator().manual_seed(cfg["seed"] * 1000 + i)))
+            for i in range(cfg["num_seqs"])]
+
+
+def decode_workload(cfg, dev):
+    """Seeded paged pools, block tables and queries on the device."""
+    import torch
+
+    dtype = getattr(torch, cfg["dtype"])
+    bs = 16
+    ctx = context_lengths(cfg)
+    need = [max(1, math.ceil(c / bs)) for c in ctx]
+    nb = math.ceil(1.1 * sum(need)) if cfg["ctx"][0] == "uniform" else sum(need)
+    g = torch.Generator().manual_seed(cfg["seed"])
+    perm = torch.randperm(nb, generator=g)
+    width = max(need)
+    table = torch.full((len(ctx), width), -1, dtype=torch.int32)
+    pos = 0
+    for i, n in enumerate(need):
+        table[i, :n] = perm[pos:pos + n].to(torch.int32)
+        pos += n
+    gd = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    shape = (nb, bs, cfg["hkv"], cfg["d"])
+    k = (torch.randn(shape, generator=gd, device=dev, dtype=torch.float32) * cfg["vscale"]).to(dtype)
+    v = (torch.randn(shape, generator=gd, device=dev, dtype=torch.float32) * cfg["vscale"]).to(dtype)
+    q = (torch.randn((len(ctx), cfg["hq"], cfg["d"]), generator=gd, device=dev,
+                     dtype=torch.float32) * cfg["vscale"]).to(dtype)
+    eb = torch.finfo(dtype).bits // 8
+    kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * eb * 2
+    qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * eb * 2
+    tbl_bytes = sum(math.ceil(c / bs) for c in ctx) * 4 + len(ctx) * 4
+    return dict(ctx=ctx, bs=bs, k=k, v=v, q=q, table=table.to(dev),
+                ctx_dev=torch.tensor(ctx, dtype=torch.int32, device=dev),
+                table_host=table, algo_bytes=kv_bytes + qo_bytes + tbl_bytes,
+                flops=4 * sum(ctx) * cfg["hq"] * cfg["d"], dtype=dtype, scale=cfg["d"] ** -0.5)
+
+
+def cpu_baseline(cfg, w, budget_s: float):
+    """The oracle's restatement of CpuAttentionBackend (fp32 upcast, grouped
+    einsum, softmax, einsum) over the batch's sequences on the host cores."""
+    import torch
+    from oracle import attention as oa
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    bs = w["bs"]
+    kc, vc, q = w["k"].cpu(), w["v"].cpu(), w["q"].cpu()
+    seqs = []
+    for i, c in enumerate(w["ctx"]):
+        kk, vv = oa.gather_context(kc, vc, w["table_host"][i].tolist(), c)
+        seqs.append((q[i], kk.contiguous(), vv.contiguous()))
+    del kc, vc
+    # One timed pass over as many sequences as fit the budget (at least one).
+    t0 = time.perf_counter()
+    done, nbytes, tokens = 0, 0, 0
+    eb = torch.finfo(w["dtype"]).bits // 8
+    for qi, kk, vv in seqs:
+        oa.attend(qi, kk, vv, w["scale"]).to(w["dtype"])
+        done += 1
+        nbytes += kk.numel() * eb * 2 + qi.numel() * eb * 2
+        tokens += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    # Same sample again with the reference's torch.cat append in front.
+    t1 = time.perf_counter()
+    for qi, kk, vv in seqs[:done]:
+        k2 = torch.cat([kk, kk[-1:]], dim=0)
+        v2 = torch.cat([vv, vv[-1:]], dim=0)
+        oa.attend(qi, k2, v2, w["scale"]).to(w["dtype"])
+    dt_cat = time.perf_counter() - t1
+    cpu_model = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": nbytes / dt / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} of {len(seqs)} sequences of the same batch, one decode step each "
+                  f"(fp32 upcast + einsum + softmax + einsum, as CpuAttentionBackend.decode_layer)",
+        "seconds": dt,
+        "tokens_per_s": tokens / dt,
+        "with_cat_append_gbs": nbytes / dt_cat / 1e9,
+        "cpu_model": cpu_model,
+    }
+
+
+def bench_decode(args, cfg):
+    import torch
+    from cloverinfer_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"building workload {args.config}")
+    w = decode_workload(cfg, dev)
+    out = torch.empty_like(w["q"])
+    max_ctx = max(w["ctx"])
+    part = args.partition if args.partition is not None else cfg["partition"]
+    if part is None:
+        hq, hkv = cfg["hq"], cfg["hkv"]
+        part = kernels.choose_partition(len(w["ctx"]), hkv, hq // hkv, max_ctx,
+                                        kernels.num_compute_units(dev))
+    a = kernels.decode_args(out, w["q"], w["k"], w["v"], w["table"], w["ctx_dev"], w["bs"],
+                            max_ctx, scale=w["scale"])
+    split = part > 0 and max_ctx > part
+    stream = torch.cuda.current_stream(dev)
+    ws = kernels.splitk_workspace(dev, kernels.workspace_bytes(a, part)) if split else None
+    lib = kernels._native.load()
+
+    def step():
+        if split:
+            kernels.paged_decode_partials(a, part, ws, stream.cuda_stream)
+            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
+        else:
+            kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
+
+    log(f"warmup {args.warmup} (partition {part if split else 0})")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = wall / args.steps * 1e3
+
+    # Per-kernel durations: HIP events on the stream the kernels run on.
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e in ev:
+        e[0].record(stream)
+        if split:
+            kernels.paged_decode_partials(a, part, ws, stream.cuda_stream)
+            e[1].record(stream)
+            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
+        else:
+            kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
+            e[1].record(stream)
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    dec_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
+    red_us = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev) * 1e3
+    log(f"step {ms:.4f} ms, decode kernel {dec_us:.1f} us, reduce {red_us:.1f} us")
+
+    value = w["algo_bytes"] / (ms * 1e-3) / 1e9
+    achieved = w["algo_bytes"] / (dec_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                         f"traffic_{args.config}.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}[cfg["dtype"]],
+        "data": "synthetic N(0,1) q/K/V, random init, seeded; no model weights",
+        "config": {
+            "workload": cfg["workload"],
+            "num_seqs": len(w["ctx"]),
+            "num_heads": cfg["hq"],
+            "num_kv_heads": cfg["hkv"],
+            "head_dim": cfg["d"],
+            "block_size": w["bs"],
+            "total_context_tokens": sum(w["ctx"]),
+            "max_context_len": max_ctx,
+            "partition_size": part if split else 0,
+            "algorithmic_bytes_per_step": w["algo_bytes"],
+            "seed": cfg["seed"],
+        },
+        "tokens_per_s": len(w["ctx"]) / (ms * 1e-3),
+        "hbm_frac_of_peak": value / PEAK_HBM_GBS,
+        "kernels_us": {"paged_decode": dec_us, "splitk_reduce": red_us if split else 0.0},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_decode_mfma" if cfg["dtype"] != "float32" else "paged_decode_valu",
+            "achieved": achieved,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBS,
+            "traffic": traffic,
+        },
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(cfg, w, args.cpu_budget)
+    return result
+
+
+def bench_prefill(args):
+    """Chunked prefill, 8 sequences x (4096 cached + 512 new), 32 q / 8 kv
+    heads, head_dim 128, bf16: a step appends the 512 new K/V rows of every
+    sequence (reshape_and_cache) and runs the causal chunk attention."""
+    import torch
+    from cloverinfer_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    S, cached, new, hq, hkv, d, bs = 8, 4096, 512, 32, 8, 128, 16
+    seed = 1005
+    ctx = [cached + new] * S
+    need = [math.ceil(c / bs) for c in ctx]
+    nb = sum(need)
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(nb, generator=g)
+    table = perm.view(S, -1).to(torch.int32).to(dev)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    v = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    q = torch.randn((S * new, hq, d), generator=gd, device=dev).to(torch.bfloat16)
+    kn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    vn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    pos = torch.arange(cached, cached + new)
+    slots = torch.cat([table[s].long().cpu()[pos // bs] * bs + pos % bs for s in range(S)]).to(dev)
+    ctx_dev = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    qsl = torch.arange(0, S * new + 1, new, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    scale = d ** -0.5
+
+    def append():
+        kernels.reshape_and_cache(kn, vn, k, v, slots)
+
+    def attend():
+        kernels.chunked_prefill(out, q, k, v, table, ctx_dev, qsl, new, scale=scale)
+
+    for _ in range(args.warmup):
+        append()
+        attend()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        append()
+        attend()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e in ev:
+        e[0].record(stream)
+        append()
+        e[1].record(stream)
+        attend()
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    app_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
+    att_us = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev) * 1e3
+    flops = 4 * d * hq * S * sum(cached + i + 1 for i in range(new))
+    achieved = flops / (att_us * 1e-6) / 1e12
+    return {
+        "metric": "chunked-prefill MFMA TFLOP/s (causal-masked flops)",
+        "value": flops / (ms * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic N(0,1), seeded",
+        "config": {"workload": "chunked prefill: 8 seqs x (4096 cached + 512 new), 32 q / 8 kv "
+                               "heads, head_dim 128, block 16, bf16, causal in chunk",
+                   "flops_per_step": flops},
+        "tokens_per_s": S * new / (ms * 1e-3),
+        "kernels_us": {"reshape_and_cache": app_us, "chunked_prefill": att_us},
+        "roofline": {"bound": "mfma", "kernel": "chunked_prefill", "achieved": achieved,
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="qwen7b",
+                    choices=sorted(DECODE_CONFIGS) + ["prefill"])
+    ap.add_argument("--partition", type=int, default=None,
+                    help="split-K partition size (0 = single pass; default: automatic)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU baseline work (a bounded sample)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the paged-attention "
+              "kernels run on a single device and this build has no multi-GPU path.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+    if args.config == "prefill":
+        result = bench_prefill(args)
+    else:
+        result = bench_decode(args, DECODE_CONFIGS[args.config])
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,190 @@
+"""ctypes binding of the C ABI in include/clover_attn.h.
+
+This module is the only place that knows the struct layouts of the C ABI.
+It loads ``cloverinfer_amd/_lib/libclover_attn.so`` (built by
+``cloverinfer_amd.build``) and fails loudly when the library is missing or
+was built for another ABI version: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+ABI_VERSION = 1
+
+CLV_F32, CLV_F16, CLV_BF16 = 0, 1, 2
+
+CLV_OK = 0
+CLV_EINVAL = 1
+CLV_EUNSUPPORTED = 2
+CLV_ELAUNCH = 3
+CLV_EWORKSPACE = 4
+
+_c_i32 = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_ptr = ctypes.c_void_p
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``clv_decode_args``."""
+
+    _fields_ = [
+        ("out", _c_ptr),
+        ("q", _c_ptr),
+        ("k_cache", _c_ptr),
+        ("v_cache", _c_ptr),
+        ("block_tables", _c_ptr),
+        ("context_lens", _c_ptr),
+        ("q_stride_seq", _c_i64),
+        ("q_stride_head", _c_i64),
+        ("out_stride_seq", _c_i64),
+        ("out_stride_head", _c_i64),
+        ("kv_stride_block", _c_i64),
+        ("kv_stride_token", _c_i64),
+        ("kv_stride_head", _c_i64),
+        ("num_seqs", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("block_size", _c_i32),
+        ("max_blocks_per_seq", _c_i32),
+        ("max_context_len", _c_i32),
+        ("num_blocks", _c_i32),
+        ("dtype", _c_i32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class CacheArgs(ctypes.Structure):
+    """Mirror of ``clv_cache_args``."""
+
+    _fields_ = [
+        ("key", _c_ptr),
+        ("value", _c_ptr),
+        ("k_cache", _c_ptr),
+        ("v_cache", _c_ptr),
+        ("slot_mapping", _c_ptr),
+        ("key_stride_token", _c_i64),
+        ("key_stride_head", _c_i64),
+        ("value_stride_token", _c_i64),
+        ("value_stride_head", _c_i64),
+        ("kv_stride_block", _c_i64),
+        ("kv_stride_token", _c_i64),
+        ("kv_stride_head", _c_i64),
+        ("num_tokens", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("block_size", _c_i32),
+        ("num_blocks", _c_i32),
+        ("dtype", _c_i32),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ``clv_prefill_args``."""
+
+    _fields_ = [
+        ("out", _c_ptr),
+        ("q", _c_ptr),
+        ("k_cache", _c_ptr),
+        ("v_cache", _c_ptr),
+        ("block_tables", _c_ptr),
+        ("context_lens", _c_ptr),
+        ("query_start_loc", _c_ptr),
+        ("q_stride_token", _c_i64),
+        ("q_stride_head", _c_i64),
+        ("out_stride_token", _c_i64),
+        ("out_stride_head", _c_i64),
+        ("kv_stride_block", _c_i64),
+        ("kv_stride_token", _c_i64),
+        ("kv_stride_head", _c_i64),
+        ("num_seqs", _c_i32),
+        ("num_tokens", _c_i32),
+        ("num_heads", _c_i32),
+        ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32),
+        ("block_size", _c_i32),
+        ("max_blocks_per_seq", _c_i32),
+        ("max_query_len", _c_i32),
+        ("num_blocks", _c_i32),
+        ("dtype", _c_i32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+# Exported symbols and their (restype, argtypes).
+SIGNATURES = {
+    "clv_abi_version": (ctypes.c_int, []),
+    "clv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "clv_reshape_and_cache": (ctypes.c_int, [ctypes.POINTER(CacheArgs), _c_ptr]),
+    "clv_paged_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _c_ptr]),
+    "clv_splitk_workspace_bytes": (ctypes.c_size_t, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "clv_paged_decode_splitk": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "clv_paged_decode_partials": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "clv_splitk_reduce": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
+    "clv_chunked_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), _c_ptr]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> str:
+    return _build.LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once; raise RuntimeError if it is absent or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{path} is missing: build it with `python -m cloverinfer_amd.build` "
+                "(there is no CPU fallback for the paged-attention kernels)"
+            )
+        # Import torch first so that its HIP runtime is the one the library binds.
+        import torch  # noqa: F401
+
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        version = lib.clv_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"{path}: ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def status_string(code: int) -> str:
+    return load().clv_status_string(code).decode()
+
+
+def check(code: int, what: str) -> None:
+    """Map a C-ABI status to the Python exception classes."""
+    if code == CLV_OK:
+        return
+    msg = f"{what}: {status_string(code)} (status {code})"
+    if code == CLV_EINVAL or code == CLV_EWORKSPACE:
+        raise ValueError(msg)
+    if code == CLV_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,110 @@
+// cache_ops.hip - KV append ("reshape_and_cache") for the paged pools.
+//
+// Token i's key/value rows [num_kv_heads, head_dim] go to cache slot
+// slot_mapping[i] = block*block_size + offset, i.e. to
+//   cache[block, offset, h, :]   for every kv head h.
+// This is the device-side form of KVCacheManager.write_new_kv's index-put
+// (src/core/memory_manager.py:131-132) and of load_initial_kv's per-block
+// copies (src/core/memory_manager.py:88-91), for any number of tokens in one
+// launch. It is a pure copy: HBM-bound, 2 reads + 2 writes of each row.
+#include "clv_device.h"
+
+namespace clv {
+namespace {
+
+constexpr int kThreads = 256;
+
+// One thread moves one 16-byte chunk of one (token, head) row of both the key
+// and the value. Rows are head_dim*elem_bytes long, a multiple of 16 bytes.
+__global__ void __launch_bounds__(kThreads)
+reshape_and_cache_vec16(const CacheParams p, int chunks_per_row) {
+  // The launcher guarantees num_tokens*num_kv_heads*chunks_per_row < 2^31.
+  const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t rows = (uint32_t)p.num_tokens * (uint32_t)p.num_kv_heads;
+  const uint32_t row = gid / (uint32_t)chunks_per_row;
+  if (row >= rows) return;
+  const int chunk = (int)(gid - row * (uint32_t)chunks_per_row);
+  const int token = (int)(row / (uint32_t)p.num_kv_heads);
+  const int head = (int)(row - (uint32_t)token * (uint32_t)p.num_kv_heads);
+  const int64_t slot = p.slot_mapping[token];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot >> p.block_shift;
+  const int64_t off = slot & ((1 << p.block_shift) - 1);
+  const int64_t eb = p.elem_bytes;
+  const int64_t dst =
+      (blk * p.kv_stride_block + off * p.kv_stride_token + head * p.kv_stride_head) * eb +
+      chunk * 16;
+  const int64_t src_k = ((int64_t)token * p.key_stride_token + head * p.key_stride_head) * eb +
+                        chunk * 16;
+  const int64_t src_v =
+      ((int64_t)token * p.value_stride_token + head * p.value_stride_head) * eb + chunk * 16;
+  const u32x4 kv = load_vec<u32x4>((const char *)p.key + src_k);
+  const u32x4 vv = load_vec<u32x4>((const char *)p.value + src_v);
+  store_vec<u32x4>((char *)p.k_cache + dst, kv);
+  store_vec<u32x4>((char *)p.v_cache + dst, vv);
+}
+
+// Element-wise fallback for rows or strides that are not 16-byte aligned.
+template <typename E>
+__global__ void __launch_bounds__(kThreads) reshape_and_cache_elem(const CacheParams p) {
+  // The launcher guarantees num_tokens*num_kv_heads*head_dim < 2^31.
+  const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t total = (uint32_t)p.num_tokens * (uint32_t)p.num_kv_heads * (uint32_t)p.head_dim;
+  if (gid >= total) return;
+  const int d = (int)(gid % (uint32_t)p.head_dim);
+  const uint32_t row = gid / (uint32_t)p.head_dim;
+  const int token = (int)(row / (uint32_t)p.num_kv_heads);
+  const int head = (int)(row - (uint32_t)token * (uint32_t)p.num_kv_heads);
+  const int64_t slot = p.slot_mapping[token];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int64_t blk = slot >> p.block_shift;
+  const int64_t off = slot & ((1 << p.block_shift) - 1);
+  const int64_t dst = blk * p.kv_stride_block + off * p.kv_stride_token + head * p.kv_stride_head + d;
+  const E *k = (const E *)p.key;
+  const E *v = (const E *)p.value;
+  ((E *)p.k_cache)[dst] = k[(int64_t)token * p.key_stride_token + head * p.key_stride_head + d];
+  ((E *)p.v_cache)[dst] = v[(int64_t)token * p.value_stride_token + head * p.value_stride_head + d];
+}
+
+bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+}  // namespace
+
+hipError_t launch_reshape_and_cache(const CacheParams &p, hipStream_t stream) {
+  if (p.num_tokens == 0 || p.num_kv_heads == 0) return hipSuccess;
+  const int64_t eb = p.elem_bytes;
+  const int64_t row_bytes = p.head_dim * eb;
+  const bool vec = row_bytes % 16 == 0 && aligned16(p.key) && aligned16(p.value) &&
+                   aligned16(p.k_cache) && aligned16(p.v_cache) &&
+                   (p.key_stride_token * eb) % 16 == 0 && (p.key_stride_head * eb) % 16 == 0 &&
+                   (p.value_stride_token * eb) % 16 == 0 &&
+                   (p.value_stride_head * eb) % 16 == 0 && (p.kv_stride_block * eb) % 16 == 0 &&
+                   (p.kv_stride_token * eb) % 16 == 0 && (p.kv_stride_head * eb) % 16 == 0;
+  const int64_t per_token = (int64_t)p.num_kv_heads * (vec ? row_bytes / 16 : p.head_dim);
+  // Keep each launch's thread count below 2^31 (32-bit index math in the kernels).
+  const int64_t tokens_per_launch = ((int64_t)1 << 30) / per_token;
+  for (int64_t t0 = 0; t0 < p.num_tokens; t0 += tokens_per_launch) {
+    CacheParams q = p;
+    const int64_t n = p.num_tokens - t0 < tokens_per_launch ? p.num_tokens - t0 : tokens_per_launch;
+    q.num_tokens = (int32_t)n;
+    q.key = (const char *)p.key + t0 * p.key_stride_token * eb;
+    q.value = (const char *)p.value + t0 * p.value_stride_token * eb;
+    q.slot_mapping = p.slot_mapping + t0;
+    const int64_t work = n * per_token;
+    const unsigned blocks = (unsigned)((work + kThreads - 1) / kThreads);
+    if (vec)
+      hipLaunchKernelGGL(reshape_and_cache_vec16, dim3(blocks), dim3(kThreads), 0, stream, q,
+                         (int)(row_bytes / 16));
+    else if (eb == 4)
+      hipLaunchKernelGGL(reshape_and_cache_elem<uint32_t>, dim3(blocks), dim3(kThreads), 0, stream,
+                         q);
+    else
+      hipLaunchKernelGGL(reshape_and_cache_elem<uint16_t>, dim3(blocks), dim3(kThreads), 0, stream,
+                         q);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
+}
+
+}  // namespace clv

@@ -1,0 +1,295 @@
+// clover_attn_abi.hip - the extern "C" boundary declared in include/clover_attn.h.
+//
+// Validates every argument block, turns it into the kernels' parameter
+// structs and dispatches. Nothing here allocates device memory or keeps state
+// between calls; errors come back as status codes.
+#include <math.h>
+#include <stddef.h>
+
+#include "clover_attn.h"
+#include "clv_internal.h"
+
+namespace {
+
+using clv::DType;
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int log2_int(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+
+bool supported_head_dim(int d) {
+  return d == 8 || d == 16 || d == 32 || d == 64 || d == 128 || d == 256;
+}
+
+int elem_bytes(int dtype) { return dtype == CLV_F32 ? 4 : 2; }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool stride16(int64_t stride, int eb) { return (stride * eb) % 16 == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Validates a decode argument block and fills the kernel parameters.
+int fill_decode(const clv_decode_args *a, clv::DecodeParams *p) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
+  if (a->num_seqs < 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 || a->head_dim <= 0)
+    return CLV_EINVAL;
+  if (a->num_heads % a->num_kv_heads != 0) return CLV_EINVAL;
+  if (!is_pow2(a->block_size)) return CLV_EUNSUPPORTED;
+  if (!supported_head_dim(a->head_dim)) return CLV_EUNSUPPORTED;
+  if (a->max_blocks_per_seq < 0 || a->max_context_len < 0 || a->num_blocks <= 0) return CLV_EINVAL;
+  if (!isfinite(a->scale)) return CLV_EINVAL;
+  if (a->num_seqs > 65535) return CLV_EUNSUPPORTED;  // grid z limit
+  const int eb = elem_bytes(a->dtype);
+  if (a->num_seqs > 0) {
+    if (!a->out || !a->q || !a->k_cache || !a->v_cache || !a->context_lens) return CLV_EINVAL;
+    if (a->max_blocks_per_seq > 0 && !a->block_tables) return CLV_EINVAL;
+    if (!aligned16(a->out) || !aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+      return CLV_EINVAL;
+    if (!stride16(a->q_stride_seq, eb) || !stride16(a->q_stride_head, eb) ||
+        !stride16(a->out_stride_seq, eb) || !stride16(a->out_stride_head, eb) ||
+        !stride16(a->kv_stride_block, eb) || !stride16(a->kv_stride_token, eb) ||
+        !stride16(a->kv_stride_head, eb))
+      return CLV_EINVAL;
+  }
+  *p = clv::DecodeParams{};
+  p->out = a->out;
+  p->q = a->q;
+  p->k_cache = a->k_cache;
+  p->v_cache = a->v_cache;
+  p->block_tables = a->block_tables;
+  p->context_lens = a->context_lens;
+  p->q_stride_seq = a->q_stride_seq;
+  p->q_stride_head = a->q_stride_head;
+  p->out_stride_seq = a->out_stride_seq;
+  p->out_stride_head = a->out_stride_head;
+  p->kv_stride_block = a->kv_stride_block;
+  p->kv_stride_token = a->kv_stride_token;
+  p->kv_stride_head = a->kv_stride_head;
+  p->num_seqs = a->num_seqs;
+  p->num_heads = a->num_heads;
+  p->num_kv_heads = a->num_kv_heads;
+  p->head_dim = a->head_dim;
+  p->group = a->num_heads / a->num_kv_heads;
+  p->n_gchunks = (int32_t)ceil_div(p->group, 16);
+  p->block_shift = log2_int(a->block_size);
+  p->max_blocks_per_seq = a->max_blocks_per_seq;
+  p->max_context_len = a->max_context_len;
+  p->num_blocks = a->num_blocks;
+  p->scale_log2 = a->scale * 1.4426950408889634f;
+  return CLV_OK;
+}
+
+int launch_decode(const clv::DecodeParams &p, int dtype, int block_size, hipStream_t stream) {
+  const DType dt = (DType)dtype;
+  hipError_t err;
+  if (clv::decode_mfma_supported(dt, p.head_dim, block_size))
+    err = clv::launch_decode_mfma(p, dt, stream);
+  else
+    err = clv::launch_decode_valu(p, dt, stream);
+  return err == hipSuccess ? CLV_OK : CLV_ELAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int clv_abi_version(void) { return CLV_ABI_VERSION; }
+
+const char *clv_status_string(int status) {
+  switch (status) {
+    case CLV_OK: return "ok";
+    case CLV_EINVAL: return "invalid argument (shape, stride, alignment, pointer or dtype)";
+    case CLV_EUNSUPPORTED: return "unsupported configuration (head_dim, block_size or size limit)";
+    case CLV_ELAUNCH: return "kernel launch failed";
+    case CLV_EWORKSPACE: return "split-K workspace missing, misaligned or too small";
+    default: return "unknown status";
+  }
+}
+
+int clv_reshape_and_cache(const clv_cache_args *a, clv_stream_t stream) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
+  if (a->num_tokens < 0 || a->num_kv_heads <= 0 || a->head_dim <= 0 || a->num_blocks <= 0)
+    return CLV_EINVAL;
+  if (!is_pow2(a->block_size)) return CLV_EUNSUPPORTED;
+  if (a->num_tokens == 0) return CLV_OK;
+  if (!a->key || !a->value || !a->k_cache || !a->v_cache || !a->slot_mapping) return CLV_EINVAL;
+  clv::CacheParams p{};
+  p.key = a->key;
+  p.value = a->value;
+  p.k_cache = a->k_cache;
+  p.v_cache = a->v_cache;
+  p.slot_mapping = a->slot_mapping;
+  p.key_stride_token = a->key_stride_token;
+  p.key_stride_head = a->key_stride_head;
+  p.value_stride_token = a->value_stride_token;
+  p.value_stride_head = a->value_stride_head;
+  p.kv_stride_block = a->kv_stride_block;
+  p.kv_stride_token = a->kv_stride_token;
+  p.kv_stride_head = a->kv_stride_head;
+  p.num_tokens = a->num_tokens;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.block_shift = log2_int(a->block_size);
+  p.num_blocks = a->num_blocks;
+  p.num_slots = (int64_t)a->num_blocks * a->block_size;
+  p.elem_bytes = elem_bytes(a->dtype);
+  return clv::launch_reshape_and_cache(p, (hipStream_t)stream) == hipSuccess ? CLV_OK
+                                                                              : CLV_ELAUNCH;
+}
+
+int clv_paged_decode(const clv_decode_args *a, clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_decode(a, &p);
+  if (st != CLV_OK) return st;
+  if (p.num_seqs == 0) return CLV_OK;
+  p.partition_size = 0;
+  return launch_decode(p, a->dtype, a->block_size, (hipStream_t)stream);
+}
+
+size_t clv_splitk_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                  int32_t max_context_len, int32_t partition_size) {
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || partition_size <= 0 ||
+      max_context_len < 0)
+    return 0;
+  const size_t parts = (size_t)(max_context_len > 0 ? ceil_div(max_context_len, partition_size) : 1);
+  const size_t rows = (size_t)num_seqs * (size_t)num_heads * parts;
+  return round256(rows * (size_t)head_dim * 4) + 2 * round256(rows * 4);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Fills the split-K fields of p from the workspace; CLV_OK or an error.
+int fill_splitk(const clv_decode_args *a, int32_t partition_size, const void *workspace,
+                size_t workspace_bytes, clv::DecodeParams *p) {
+  if (partition_size <= 0 || partition_size % 32 != 0) return CLV_EINVAL;
+  const size_t need = clv_splitk_workspace_bytes(a->num_seqs, a->num_heads, a->head_dim,
+                                                 a->max_context_len, partition_size);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u) != 0)
+    return CLV_EWORKSPACE;
+  const int64_t parts = a->max_context_len > 0 ? ceil_div(a->max_context_len, partition_size) : 1;
+  if (parts > 65535) return CLV_EUNSUPPORTED;
+  const size_t rows = (size_t)a->num_seqs * (size_t)a->num_heads * (size_t)parts;
+  char *ws = (char *)workspace;
+  p->partition_size = partition_size;
+  p->max_parts = (int32_t)parts;
+  p->ws_o = (float *)ws;
+  p->ws_m = (float *)(ws + round256(rows * (size_t)a->head_dim * 4));
+  p->ws_l = (float *)(ws + round256(rows * (size_t)a->head_dim * 4) + round256(rows * 4));
+  return CLV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int clv_paged_decode_partials(const clv_decode_args *a, int32_t partition_size, void *workspace,
+                              size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  int st = fill_decode(a, &p);
+  if (st != CLV_OK) return st;
+  if (p.num_seqs == 0) return partition_size > 0 && partition_size % 32 == 0 ? CLV_OK : CLV_EINVAL;
+  st = fill_splitk(a, partition_size, workspace, workspace_bytes, &p);
+  if (st != CLV_OK) return st;
+  return launch_decode(p, a->dtype, a->block_size, (hipStream_t)stream);
+}
+
+int clv_splitk_reduce(const clv_decode_args *a, int32_t partition_size, const void *workspace,
+                      size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  int st = fill_decode(a, &p);
+  if (st != CLV_OK) return st;
+  if (p.num_seqs == 0) return partition_size > 0 && partition_size % 32 == 0 ? CLV_OK : CLV_EINVAL;
+  st = fill_splitk(a, partition_size, workspace, workspace_bytes, &p);
+  if (st != CLV_OK) return st;
+  return clv::launch_splitk_reduce(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
+}
+
+int clv_paged_decode_splitk(const clv_decode_args *a, int32_t partition_size, void *workspace,
+                            size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_decode(a, &p);
+  if (st != CLV_OK) return st;
+  if (partition_size <= 0 || partition_size % 32 != 0) return CLV_EINVAL;
+  if (p.num_seqs == 0) return CLV_OK;
+  // A context that fits one partition needs no merge.
+  if (a->max_context_len <= partition_size) {
+    p.partition_size = 0;
+    return launch_decode(p, a->dtype, a->block_size, (hipStream_t)stream);
+  }
+  const int rc = clv_paged_decode_partials(a, partition_size, workspace, workspace_bytes, stream);
+  if (rc != CLV_OK) return rc;
+  return clv_splitk_reduce(a, partition_size, workspace, workspace_bytes, stream);
+}
+
+int clv_chunked_prefill(const clv_prefill_args *a, clv_stream_t stream) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
+  if (a->num_seqs < 0 || a->num_tokens < 0 || a->num_heads <= 0 || a->num_kv_heads <= 0 ||
+      a->head_dim <= 0 || a->num_blocks <= 0 || a->max_blocks_per_seq < 0 || a->max_query_len < 0)
+    return CLV_EINVAL;
+  if (a->num_heads % a->num_kv_heads != 0) return CLV_EINVAL;
+  if (!is_pow2(a->block_size)) return CLV_EUNSUPPORTED;
+  if (!supported_head_dim(a->head_dim)) return CLV_EUNSUPPORTED;
+  if (!isfinite(a->scale)) return CLV_EINVAL;
+  if (a->num_seqs > 65535) return CLV_EUNSUPPORTED;
+  if (a->num_seqs == 0 || a->num_tokens == 0) return CLV_OK;
+  const int eb = elem_bytes(a->dtype);
+  if (!a->out || !a->q || !a->k_cache || !a->v_cache || !a->context_lens || !a->query_start_loc)
+    return CLV_EINVAL;
+  if (a->max_blocks_per_seq > 0 && !a->block_tables) return CLV_EINVAL;
+  if (!aligned16(a->out) || !aligned16(a->q) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+    return CLV_EINVAL;
+  if (!stride16(a->q_stride_token, eb) || !stride16(a->q_stride_head, eb) ||
+      !stride16(a->out_stride_token, eb) || !stride16(a->out_stride_head, eb) ||
+      !stride16(a->kv_stride_block, eb) || !stride16(a->kv_stride_token, eb) ||
+      !stride16(a->kv_stride_head, eb))
+    return CLV_EINVAL;
+  clv::PrefillParams p{};
+  p.out = a->out;
+  p.q = a->q;
+  p.k_cache = a->k_cache;
+  p.v_cache = a->v_cache;
+  p.block_tables = a->block_tables;
+  p.context_lens = a->context_lens;
+  p.query_start_loc = a->query_start_loc;
+  p.q_stride_token = a->q_stride_token;
+  p.q_stride_head = a->q_stride_head;
+  p.out_stride_token = a->out_stride_token;
+  p.out_stride_head = a->out_stride_head;
+  p.kv_stride_block = a->kv_stride_block;
+  p.kv_stride_token = a->kv_stride_token;
+  p.kv_stride_head = a->kv_stride_head;
+  p.num_seqs = a->num_seqs;
+  p.num_tokens = a->num_tokens;
+  p.num_heads = a->num_heads;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.group = a->num_heads / a->num_kv_heads;
+  p.block_shift = log2_int(a->block_size);
+  p.max_blocks_per_seq = a->max_blocks_per_seq;
+  p.max_query_len = a->max_query_len;
+  p.num_blocks = a->num_blocks;
+  p.scale_log2 = a->scale * 1.4426950408889634f;
+  const DType dt = (DType)a->dtype;
+  hipError_t err;
+  if (clv::prefill_mfma_supported(dt, a->head_dim, a->block_size))
+    err = clv::launch_prefill_mfma(p, dt, (hipStream_t)stream);
+  else
+    err = clv::launch_prefill_valu(p, dt, (hipStream_t)stream);
+  return err == hipSuccess ? CLV_OK : CLV_ELAUNCH;
+}
+
+}  // extern "C"

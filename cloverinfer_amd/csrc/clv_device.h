@@ -1,0 +1,129 @@
+// clv_device.h - device-side helpers shared by the gfx950 attention kernels.
+//
+// Storage types are the clang builtin 16-bit floats (__bf16, _Float16) and
+// float; every kernel computes in fp32. Vector types are clang ext_vector
+// types so that MFMA builtins take them directly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "clv_internal.h"
+
+namespace clv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  // v_exp_f32: exact 0 for -inf, 1 for 0.
+  return __builtin_amdgcn_exp2f(x);
+}
+
+// ---------------------------------------------------------------- conversions
+template <typename T> __device__ __forceinline__ float to_f32(T x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// Unpack a 32-bit word holding two 16-bit values (low half first).
+template <typename T> __device__ __forceinline__ float lo16_to_f32(uint32_t w);
+template <typename T> __device__ __forceinline__ float hi16_to_f32(uint32_t w);
+
+template <> __device__ __forceinline__ float lo16_to_f32<__bf16>(uint32_t w) {
+  return __builtin_bit_cast(float, w << 16);
+}
+template <> __device__ __forceinline__ float hi16_to_f32<__bf16>(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+template <> __device__ __forceinline__ float lo16_to_f32<_Float16>(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+template <> __device__ __forceinline__ float hi16_to_f32<_Float16>(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// ---------------------------------------------------------------- MFMA
+// v_mfma_f32_16x16x32_{bf16,f16} (gfx950). Operand layout for lane l:
+//   A (16 x 32, row-major M x K): row l%16, k = 8*(l/16) .. +8
+//   B (32 x 16, K x N):           col l%16, k = 8*(l/16) .. +8
+//   C/D (16 x 16):                col l%16, rows 4*(l/16) .. +4
+template <typename T> struct Mfma16x16x32;
+
+template <> struct Mfma16x16x32<__bf16> {
+  typedef bf16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma16x16x32<_Float16> {
+  typedef f16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// v_mfma_f32_32x32x16_{bf16,f16} (gfx950). Operand layout for lane l:
+//   A (32 x 16): row l%32, k = 8*(l/32) .. +8
+//   B (16 x 32): col l%32, k = 8*(l/32) .. +8
+//   C/D (32 x 32): col l%32, rows {8*q + 4*(l/32) + r : q = 0..3, r = 0..3}
+//   (register 4*q + r).
+template <typename T> struct Mfma32x32x16;
+
+template <> struct Mfma32x32x16<__bf16> {
+  typedef bf16x8 op_t;
+  static __device__ __forceinline__ f32x16 run(op_t a, op_t b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma32x32x16<_Float16> {
+  typedef f16x8 op_t;
+  static __device__ __forceinline__ f32x16 run(op_t a, op_t b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Pack 8 fp32 values into an MFMA 16-bit operand (round to nearest even).
+template <typename T>
+__device__ __forceinline__ typename Mfma16x16x32<T>::op_t pack8(const float (&x)[8]) {
+  typename Mfma16x16x32<T>::op_t r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (T)x[i];
+  return r;
+}
+
+// Two 16-bit halves, one from each word: (lo(a), lo(b)) or (hi(a), hi(b)).
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+__device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, 64); }
+
+// ---------------------------------------------------------------- memory
+template <typename V>
+__device__ __forceinline__ V load_vec(const void *p) {
+  return *reinterpret_cast<const V *>(p);
+}
+
+template <typename V>
+__device__ __forceinline__ void store_vec(void *p, V v) {
+  *reinterpret_cast<V *>(p) = v;
+}
+
+}  // namespace clv

@@ -1,0 +1,79 @@
+// clv_internal.h - kernel parameter blocks and launcher declarations shared
+// by the C-ABI layer (clover_attn_abi.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace clv {
+
+// Decode parameters after validation. Strides are in elements.
+struct DecodeParams {
+  void *out;
+  const void *q;
+  const void *k_cache;
+  const void *v_cache;
+  const int32_t *block_tables;
+  const int32_t *context_lens;
+  int64_t q_stride_seq, q_stride_head;
+  int64_t out_stride_seq, out_stride_head;
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  int32_t num_seqs, num_heads, num_kv_heads, head_dim;
+  int32_t group;          // num_heads / num_kv_heads
+  int32_t n_gchunks;      // ceil(group / 16): query-head chunks per kv head
+  int32_t block_shift;    // log2(block_size)
+  int32_t max_blocks_per_seq, max_context_len, num_blocks;
+  float scale_log2;       // scale * log2(e): scores live in the log2 domain
+  // Split-K: partition_size > 0 writes partials to the workspace.
+  int32_t partition_size; // tokens per workgroup, multiple of 32; 0 = whole context
+  int32_t max_parts;      // partitions per sequence held by the workspace
+  float *ws_o;            // [num_seqs, num_heads, max_parts, head_dim] normalised contexts
+  float *ws_m;            // [num_seqs, num_heads, max_parts] row max (natural-log domain)
+  float *ws_l;            // [num_seqs, num_heads, max_parts] row sum
+};
+
+struct CacheParams {
+  const void *key;
+  const void *value;
+  void *k_cache;
+  void *v_cache;
+  const int64_t *slot_mapping;
+  int64_t key_stride_token, key_stride_head;
+  int64_t value_stride_token, value_stride_head;
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  int32_t num_tokens, num_kv_heads, head_dim, block_shift, num_blocks;
+  int64_t num_slots;      // num_blocks * block_size
+  int32_t elem_bytes;
+};
+
+struct PrefillParams {
+  void *out;
+  const void *q;
+  const void *k_cache;
+  const void *v_cache;
+  const int32_t *block_tables;
+  const int32_t *context_lens;
+  const int32_t *query_start_loc;
+  int64_t q_stride_token, q_stride_head;
+  int64_t out_stride_token, out_stride_head;
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  int32_t num_seqs, num_tokens, num_heads, num_kv_heads, head_dim;
+  int32_t group, block_shift, max_blocks_per_seq, max_query_len, num_blocks;
+  float scale_log2;
+};
+
+enum class DType : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+// Launchers return hipSuccess or the launch error. Shapes are pre-validated.
+hipError_t launch_reshape_and_cache(const CacheParams &p, hipStream_t stream);
+hipError_t launch_decode_mfma(const DecodeParams &p, DType dt, hipStream_t stream);
+hipError_t launch_decode_valu(const DecodeParams &p, DType dt, hipStream_t stream);
+hipError_t launch_splitk_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
+hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream);
+hipError_t launch_prefill_valu(const PrefillParams &p, DType dt, hipStream_t stream);
+
+// Whether the MFMA decode kernel covers this shape/dtype.
+bool decode_mfma_supported(DType dt, int head_dim, int block_size);
+bool prefill_mfma_supported(DType dt, int head_dim, int block_size);
+
+}  // namespace clv

@@ -1,0 +1,294 @@
+"""Tensor-level entry points over the C ABI (the ``clover_kernels`` mirror).
+
+``paged_attention`` keeps the reference binding's signature and meaning
+(src/kernels/csrc/manager.cpp:19-38): the caller allocates ``out``, sizes come
+from the tensors, the call is asynchronous on the current stream and returns
+nothing. The other functions are the new operations of the hot path. Every
+call goes through ``libclover_attn.so``; tensors must live on a HIP device.
+"""
+from __future__ import annotations
+
+import math
+import threading
+
+import torch
+
+from . import _native
+
+_DTYPES = {
+    torch.float32: _native.CLV_F32,
+    torch.float16: _native.CLV_F16,
+    torch.bfloat16: _native.CLV_BF16,
+}
+
+# Tokens per split-K partition when the caller does not choose one.
+DEFAULT_PARTITION = 512
+
+_ws_lock = threading.Lock()
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_num_cus: dict[int, int] = {}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected float32, float16 or bfloat16")
+
+
+def _require_device(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            "paged-attention kernels run on a HIP device only; got tensors on "
+            f"{dev} (there is no CPU fallback)"
+        )
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, found one on {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError(
+            "k_cache and v_cache must both be [num_blocks, block_size, num_kv_heads, head_dim]"
+        )
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share strides")
+    if k_cache.stride(3) != 1:
+        raise ValueError("the cache head_dim must be contiguous")
+    if v_cache.dtype != k_cache.dtype:
+        raise ValueError("k_cache and v_cache dtypes differ")
+
+
+def num_compute_units(dev: torch.device) -> int:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _num_cus:
+        _num_cus[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _num_cus[idx]
+
+
+def choose_partition(num_seqs: int, num_kv_heads: int, group: int, max_context_len: int,
+                     num_cus: int) -> int:
+    """Split-K partition size (0 = single pass) for a decode batch.
+
+    A single pass launches one workgroup per (sequence, kv head, group
+    chunk); it is used when that already gives every compute unit several
+    workgroups and contexts are short enough to stay balanced.
+    """
+    if max_context_len <= DEFAULT_PARTITION:
+        return 0
+    single = num_seqs * num_kv_heads * ((group + 15) // 16)
+    if single >= 4 * num_cus:
+        return 0
+    return DEFAULT_PARTITION
+
+
+def splitk_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """A cached, grow-only uint8 workspace of at least ``nbytes`` for the
+    current stream of ``dev`` (one per stream, so that launches on different
+    streams never share partials)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _stream(torch.device("cuda", idx)))
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+            _workspaces[key] = ws
+    return ws
+
+
+def _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                 max_context_len, scale) -> _native.DecodeArgs:
+    if q.dim() != 3 or out.shape != q.shape:
+        raise ValueError("q and out must both be [num_seqs, num_heads, head_dim]")
+    _check_cache(k_cache, v_cache)
+    num_seqs, num_heads, head_dim = q.shape
+    num_blocks, bs, num_kv_heads, kd = k_cache.shape
+    if kd != head_dim:
+        raise ValueError(f"head_dim mismatch: q has {head_dim}, cache has {kd}")
+    if bs != block_size:
+        raise ValueError(f"block_size {block_size} does not match the cache ({bs})")
+    if num_heads % num_kv_heads:
+        raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {num_kv_heads}")
+    if q.dtype != k_cache.dtype or out.dtype != q.dtype:
+        raise ValueError("q, out and the caches must share one dtype")
+    if q.stride(2) != 1 or out.stride(2) != 1:
+        raise ValueError("q and out need a contiguous head_dim")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise ValueError("block_tables and context_lens must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != num_seqs or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be a contiguous [num_seqs, max_blocks_per_seq] tensor")
+    if context_lens.shape != (num_seqs,) or not context_lens.is_contiguous():
+        raise ValueError("context_lens must be a contiguous [num_seqs] tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    a = _native.DecodeArgs()
+    a.out = out.data_ptr()
+    a.q = q.data_ptr()
+    a.k_cache = k_cache.data_ptr()
+    a.v_cache = v_cache.data_ptr()
+    a.block_tables = block_tables.data_ptr()
+    a.context_lens = context_lens.data_ptr()
+    a.q_stride_seq, a.q_stride_head = q.stride(0), q.stride(1)
+    a.out_stride_seq, a.out_stride_head = out.stride(0), out.stride(1)
+    a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k_cache.stride()[:3]
+    a.num_seqs, a.num_heads, a.num_kv_heads, a.head_dim = num_seqs, num_heads, num_kv_heads, head_dim
+    a.block_size = block_size
+    a.max_blocks_per_seq = block_tables.shape[1]
+    a.max_context_len = int(max_context_len)
+    a.num_blocks = num_blocks
+    a.dtype = _dtype_code(q)
+    a.scale = float(scale)
+    return a
+
+
+def decode_args(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, block_tables: torch.Tensor, context_lens: torch.Tensor,
+                block_size: int, max_context_len: int,
+                scale: float | None = None) -> _native.DecodeArgs:
+    """Validated C-ABI argument block of a paged decode (tensors stay owned
+    by the caller and must outlive every launch made with it)."""
+    _require_device(out, q, k_cache, v_cache, block_tables, context_lens)
+    return _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                        max_context_len, scale)
+
+
+def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor, block_size: int, max_context_len: int,
+                    scale: float | None = None, partition_size: int | None = None) -> None:
+    """``out[s,h] = softmax(scale * q[s,h] . K^T) V`` over each sequence's paged context.
+
+    Same arguments as the reference op (src/kernels/csrc/manager.cpp:19-27);
+    ``scale`` defaults to 1/sqrt(head_dim) as in src/kernels/csrc/attention.cu:60.
+    GQA follows from ``k_cache.shape[2] < q.shape[1]``. ``partition_size``:
+    None picks one, 0 forces a single pass, a positive multiple of 32 forces
+    split-K with that many tokens per partition.
+    """
+    dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens)
+    a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                     max_context_len, scale)
+    lib = _native.load()
+    if partition_size is None:
+        partition_size = choose_partition(a.num_seqs, a.num_kv_heads,
+                                          a.num_heads // a.num_kv_heads, a.max_context_len,
+                                          num_compute_units(dev))
+    stream = _stream(dev)
+    if partition_size == 0 or a.max_context_len <= partition_size:
+        _native.check(lib.clv_paged_decode(a, stream), "clv_paged_decode")
+        return
+    ws = splitk_workspace(dev, workspace_bytes(a, partition_size))
+    _native.check(
+        lib.clv_paged_decode_splitk(a, partition_size, ws.data_ptr(), ws.numel(), stream),
+        "clv_paged_decode_splitk",
+    )
+
+
+def workspace_bytes(a: _native.DecodeArgs, partition_size: int) -> int:
+    return _native.load().clv_splitk_workspace_bytes(a.num_seqs, a.num_heads, a.head_dim,
+                                                     a.max_context_len, partition_size)
+
+
+def paged_decode_partials(a: _native.DecodeArgs, partition_size: int, workspace: torch.Tensor,
+                          stream: int) -> None:
+    """First half of split-K (partials into ``workspace``), see clv_paged_decode_partials."""
+    _native.check(_native.load().clv_paged_decode_partials(
+        a, partition_size, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        stream), "clv_paged_decode_partials")
+
+
+def splitk_reduce(a: _native.DecodeArgs, partition_size: int, workspace: torch.Tensor,
+                  stream: int) -> None:
+    """Second half of split-K (merge into ``out``), see clv_splitk_reduce."""
+    _native.check(_native.load().clv_splitk_reduce(
+        a, partition_size, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        stream), "clv_splitk_reduce")
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Write token i's ``key[i]``/``value[i]`` ([num_kv_heads, head_dim]) to cache slot
+    ``slot_mapping[i]`` (= block*block_size + offset; negative slots are skipped)."""
+    dev = _require_device(key, value, k_cache, v_cache, slot_mapping)
+    _check_cache(k_cache, v_cache)
+    num_blocks, bs, num_kv_heads, head_dim = k_cache.shape
+    if key.dim() != 3 or value.shape != key.shape or key.shape[1:] != (num_kv_heads, head_dim):
+        raise ValueError(
+            f"key/value must be [num_tokens, {num_kv_heads}, {head_dim}], got "
+            f"{tuple(key.shape)} and {tuple(value.shape)}"
+        )
+    if key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
+        raise ValueError("key/value dtype must match the cache dtype")
+    if key.stride(2) != 1 or value.stride(2) != 1:
+        raise ValueError("key/value need a contiguous head_dim")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (key.shape[0],) \
+            or not slot_mapping.is_contiguous():
+        raise ValueError("slot_mapping must be a contiguous int64 [num_tokens] tensor")
+    a = _native.CacheArgs()
+    a.key, a.value = key.data_ptr(), value.data_ptr()
+    a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    a.slot_mapping = slot_mapping.data_ptr()
+    a.key_stride_token, a.key_stride_head = key.stride(0), key.stride(1)
+    a.value_stride_token, a.value_stride_head = value.stride(0), value.stride(1)
+    a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k_cache.stride()[:3]
+    a.num_tokens = key.shape[0]
+    a.num_kv_heads, a.head_dim, a.block_size, a.num_blocks = num_kv_heads, head_dim, bs, num_blocks
+    a.dtype = _dtype_code(k_cache)
+    _native.check(_native.load().clv_reshape_and_cache(a, _stream(dev)), "clv_reshape_and_cache")
+
+
+def chunked_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor, query_start_loc: torch.Tensor,
+                    max_query_len: int, scale: float | None = None) -> None:
+    """Causal attention of each sequence's new query rows over its paged context.
+
+    Sequence s owns rows ``query_start_loc[s]:query_start_loc[s+1]`` of q/out;
+    its new tokens are the last ones of its ``context_lens[s]`` cached tokens,
+    and row i sees positions ``<= context_lens[s] - n_s + i``.
+    """
+    dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens, query_start_loc)
+    _check_cache(k_cache, v_cache)
+    if q.dim() != 3 or out.shape != q.shape:
+        raise ValueError("q and out must both be [num_tokens, num_heads, head_dim]")
+    num_tokens, num_heads, head_dim = q.shape
+    num_blocks, bs, num_kv_heads, kd = k_cache.shape
+    if kd != head_dim or num_heads % num_kv_heads:
+        raise ValueError("q and the caches disagree on head_dim or the GQA grouping")
+    if q.dtype != k_cache.dtype or out.dtype != q.dtype:
+        raise ValueError("q, out and the caches must share one dtype")
+    if q.stride(2) != 1 or out.stride(2) != 1:
+        raise ValueError("q and out need a contiguous head_dim")
+    num_seqs = context_lens.shape[0]
+    for name, t, shape in (("context_lens", context_lens, (num_seqs,)),
+                           ("query_start_loc", query_start_loc, (num_seqs + 1,))):
+        if t.dtype != torch.int32 or t.shape != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 tensor of shape {shape}")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 \
+            or block_tables.shape[0] != num_seqs or not block_tables.is_contiguous():
+        raise ValueError("block_tables must be a contiguous int32 [num_seqs, max_blocks] tensor")
+    if scale is None:
+        scale = 1.0 / math.sqrt(head_dim)
+    a = _native.PrefillArgs()
+    a.out, a.q = out.data_ptr(), q.data_ptr()
+    a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    a.block_tables = block_tables.data_ptr()
+    a.context_lens = context_lens.data_ptr()
+    a.query_start_loc = query_start_loc.data_ptr()
+    a.q_stride_token, a.q_stride_head = q.stride(0), q.stride(1)
+    a.out_stride_token, a.out_stride_head = out.stride(0), out.stride(1)
+    a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k_cache.stride()[:3]
+    a.num_seqs, a.num_tokens, a.num_heads, a.num_kv_heads = num_seqs, num_tokens, num_heads, num_kv_heads
+    a.head_dim, a.block_size = head_dim, bs
+    a.max_blocks_per_seq = block_tables.shape[1]
+    a.max_query_len = int(max_query_len)
+    a.num_blocks = num_blocks
+    a.dtype = _dtype_code(q)
+    a.scale = float(scale)
+    _native.check(_native.load().clv_chunked_prefill(a, _stream(dev)), "clv_chunked_prefill")

@@ -1,0 +1,194 @@
+/*
+ * clover_attn.h - C ABI of the MI355X (gfx950) paged-attention hot path.
+ *
+ * Plain C: raw device pointers, element strides and sizes; no torch or HIP
+ * types in any signature. Every entry point is stream-ordered (it enqueues
+ * work on `stream` and returns), reentrant, and keeps no mutable global
+ * state. The caller owns every device buffer, including the split-K
+ * workspace, which it sizes with clv_splitk_workspace_bytes().
+ *
+ * Cache layout (shared by the key and the value pool):
+ *     [num_blocks, block_size, num_kv_heads, head_dim]
+ * addressed as  base + block*kv_stride_block + offset*kv_stride_token
+ *                    + kv_head*kv_stride_head + d     (head_dim contiguous).
+ * A token at logical position t of sequence s lives in physical block
+ * block_tables[s*max_blocks_per_seq + t/block_size], offset t%block_size.
+ *
+ * GQA: query head h reads kv head h / (num_heads/num_kv_heads), the same
+ * grouping as transformers' repeat_kv.
+ *
+ * Status codes are returned, never thrown.
+ */
+#ifndef CLOVER_ATTN_H
+#define CLOVER_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CLV_ABI_VERSION 1
+
+/* A hipStream_t; NULL selects the null stream. */
+typedef void *clv_stream_t;
+
+enum clv_dtype { CLV_F32 = 0, CLV_F16 = 1, CLV_BF16 = 2 };
+
+enum clv_status {
+  CLV_OK = 0,
+  CLV_EINVAL = 1,       /* bad shape, stride, pointer or dtype */
+  CLV_EUNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim) */
+  CLV_ELAUNCH = 3,      /* the HIP runtime rejected a launch */
+  CLV_EWORKSPACE = 4    /* split-K workspace missing or too small */
+};
+
+/*
+ * Paged decode: one query row per sequence attends to that sequence's first
+ * context_lens[s] cached tokens.
+ *   out[s, h, :] = softmax_t(scale * q[s,h,:].K[t,kvh,:]) . V[t,kvh,:]
+ * Math is fp32 whatever the storage dtype; out is written in `dtype`.
+ * A sequence with context length 0 gets an all-zero row.
+ * Block-table entries outside [0, num_blocks) inside the context are
+ * treated as masked tokens (never dereferenced).
+ * context_lens[s] must not exceed max_context_len (larger values are
+ * clamped to it and to max_blocks_per_seq*block_size).
+ */
+typedef struct clv_decode_args {
+  void *out;                   /* [num_seqs, num_heads, head_dim]           */
+  const void *q;               /* [num_seqs, num_heads, head_dim]           */
+  const void *k_cache;         /* [num_blocks, block_size, num_kv_heads, D] */
+  const void *v_cache;         /* same layout and strides as k_cache        */
+  const int32_t *block_tables; /* [num_seqs, max_blocks_per_seq], -1 pad    */
+  const int32_t *context_lens; /* [num_seqs]                                */
+  int64_t q_stride_seq, q_stride_head;       /* elements */
+  int64_t out_stride_seq, out_stride_head;   /* elements */
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head; /* elements */
+  int32_t num_seqs, num_heads, num_kv_heads, head_dim;
+  int32_t block_size, max_blocks_per_seq, max_context_len, num_blocks;
+  int32_t dtype; /* enum clv_dtype, shared by q, out and both caches */
+  float scale;   /* softmax scale applied to q.k (1/sqrt(D) in the reference op) */
+} clv_decode_args;
+
+/*
+ * KV append ("reshape_and_cache"): copies token i's key/value rows into
+ * cache slot slot_mapping[i] = block*block_size + offset.
+ * A negative slot, or one >= num_blocks*block_size, skips the token.
+ */
+typedef struct clv_cache_args {
+  const void *key;             /* [num_tokens, num_kv_heads, head_dim] */
+  const void *value;           /* [num_tokens, num_kv_heads, head_dim] */
+  void *k_cache;               /* [num_blocks, block_size, num_kv_heads, D] */
+  void *v_cache;
+  const int64_t *slot_mapping; /* [num_tokens] */
+  int64_t key_stride_token, key_stride_head;     /* elements */
+  int64_t value_stride_token, value_stride_head; /* elements */
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head; /* elements */
+  int32_t num_tokens, num_kv_heads, head_dim, block_size, num_blocks;
+  int32_t dtype;
+} clv_cache_args;
+
+/*
+ * Chunked prefill over paged KV. Sequence s owns query rows
+ * [query_start_loc[s], query_start_loc[s+1]) of q/out; its n_s new tokens
+ * are the LAST n_s of its context_lens[s] cached tokens (append them with
+ * clv_reshape_and_cache first). Query row i of sequence s (0 <= i < n_s)
+ * attends to cached positions p <= context_lens[s] - n_s + i (causal inside
+ * the chunk, full view of everything cached before it).
+ */
+typedef struct clv_prefill_args {
+  void *out;                      /* [num_tokens, num_heads, head_dim] */
+  const void *q;                  /* [num_tokens, num_heads, head_dim] */
+  const void *k_cache;
+  const void *v_cache;
+  const int32_t *block_tables;    /* [num_seqs, max_blocks_per_seq] */
+  const int32_t *context_lens;    /* [num_seqs], including the new tokens */
+  const int32_t *query_start_loc; /* [num_seqs + 1], non-decreasing */
+  int64_t q_stride_token, q_stride_head;     /* elements */
+  int64_t out_stride_token, out_stride_head; /* elements */
+  int64_t kv_stride_block, kv_stride_token, kv_stride_head;
+  int32_t num_seqs, num_tokens, num_heads, num_kv_heads, head_dim;
+  int32_t block_size, max_blocks_per_seq, max_query_len, num_blocks;
+  int32_t dtype;
+  float scale;
+} clv_prefill_args;
+
+/* ABI version of the loaded library (CLV_ABI_VERSION at build time). */
+int clv_abi_version(void);
+
+/* Static text for a status code. */
+const char *clv_status_string(int status);
+
+/*
+ * Replaces the per-token Python index-put of KVCacheManager.write_new_kv
+ * (src/core/memory_manager.py:123-132) and the per-block copies of
+ * load_initial_kv (src/core/memory_manager.py:74-93): one launch for any
+ * number of tokens.
+ */
+int clv_reshape_and_cache(const clv_cache_args *args, clv_stream_t stream);
+
+/*
+ * Replaces clover_kernels.paged_attention (src/kernels/csrc/manager.cpp:19-42,
+ * launcher src/kernels/csrc/attention.cu:118-149) with GQA, bf16 and an
+ * explicit scale. Single pass: one workgroup per (sequence, kv head) walks
+ * the whole context. Needs no workspace.
+ */
+int clv_paged_decode(const clv_decode_args *args, clv_stream_t stream);
+
+/*
+ * Bytes of workspace clv_paged_decode_splitk needs: per (sequence, query
+ * head, partition) one fp32 context row plus its row max and row sum.
+ */
+size_t clv_splitk_workspace_bytes(int32_t num_seqs, int32_t num_heads,
+                                  int32_t head_dim, int32_t max_context_len,
+                                  int32_t partition_size);
+
+/*
+ * Split-K decode: the context is cut into partitions of partition_size
+ * tokens (a positive multiple of 32); each (sequence, kv head, partition)
+ * produces a normalised partial context with its row max and row sum, and a
+ * second kernel merges them with the log-sum-exp rule of the reference's
+ * partial-softmax merge (src/core/resident_kv_store.py:2497-2509).
+ * Equal to clv_paged_decode_partials followed by clv_splitk_reduce (when
+ * max_context_len <= partition_size it runs the single pass instead).
+ * No counterpart kernel exists in the reference.
+ */
+int clv_paged_decode_splitk(const clv_decode_args *args, int32_t partition_size,
+                            void *workspace, size_t workspace_bytes,
+                            clv_stream_t stream);
+
+/*
+ * First half of split-K: writes, for every (sequence s, query head h,
+ * partition p < ceil(context_lens[s]/partition_size)), the normalised
+ * partial context, its row max (natural-log domain, of scale*q.k) and row
+ * sum into the workspace. `out` is not touched. Replaces the per-segment
+ * partial attention of src/core/resident_kv_store.py:715-783.
+ */
+int clv_paged_decode_partials(const clv_decode_args *args, int32_t partition_size,
+                              void *workspace, size_t workspace_bytes,
+                              clv_stream_t stream);
+
+/*
+ * Second half of split-K: merges the partials clv_paged_decode_partials left
+ * in the workspace (same args, partition_size and workspace) into `out`.
+ * Restates src/core/resident_kv_store.py:2497-2509 over all partitions:
+ *   M = max m_i, w_i = l_i e^(m_i - M), out = sum c_i w_i / max(sum w_i, 1e-12).
+ */
+int clv_splitk_reduce(const clv_decode_args *args, int32_t partition_size,
+                      const void *workspace, size_t workspace_bytes,
+                      clv_stream_t stream);
+
+/*
+ * Chunked prefill over paged KV (MFMA for fp16/bf16). No counterpart in the
+ * reference; defined as equal, row by row, to successive append-then-attend
+ * decode steps of CpuAttentionBackend.decode_layer
+ * (src/core/attention_backend.py:82-123).
+ */
+int clv_chunked_prefill(const clv_prefill_args *args, clv_stream_t stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* CLOVER_ATTN_H */

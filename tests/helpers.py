@@ -1,0 +1,68 @@
+"""Shared test helpers: seeded paged-KV construction and the parity bar."""
+from __future__ import annotations
+
+import math
+
+import torch
+
+# Parity bar for attention outputs against the fp32 oracle: max-abs 2e-3, and
+# 1e-2 relative where the reference value is at least 0.2 in magnitude (a pure
+# relative bound on near-zero 16-bit outputs is ill-posed).
+ATOL = 2e-3
+RTOL = 1e-2
+REL_FLOOR = 0.2
+
+
+def assert_attention_close(got: torch.Tensor, ref: torch.Tensor, atol: float = ATOL,
+                           rtol: float = RTOL, what: str = "") -> None:
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} != {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{what}: non-finite output"
+    err = (got - ref).abs()
+    max_abs = err.max().item() if err.numel() else 0.0
+    big = ref.abs() >= REL_FLOOR
+    max_rel = (err[big] / ref.abs()[big]).max().item() if big.any() else 0.0
+    assert max_abs <= atol, f"{what}: max-abs {max_abs:.3e} > {atol:.1e}"
+    assert max_rel <= rtol, f"{what}: max-rel {max_rel:.3e} > {rtol:.1e}"
+
+
+def make_paged_kv(seed: int, context_lens, num_kv_heads: int, head_dim: int, block_size: int,
+                  dtype: torch.dtype, value_scale: float = 1.0, spare_blocks: int = 0,
+                  pool_slack: float = 0.0):
+    """Random paged pools and block tables (CPU tensors).
+
+    Every sequence gets ceil(ctx / bs) blocks (at least one) drawn without
+    replacement from a shuffled pool; unused slots hold NaN so that a kernel
+    reading outside a context shows up in its output. Returns
+    (k_cache, v_cache, tables: list[list[int]]).
+    """
+    g = torch.Generator().manual_seed(seed)
+    need = [max(1, math.ceil(c / block_size)) for c in context_lens]
+    nb = int(math.ceil(sum(need) * (1.0 + pool_slack))) + spare_blocks
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables, pos = [], 0
+    for n in need:
+        tables.append(perm[pos:pos + n])
+        pos += n
+    shape = (nb, block_size, num_kv_heads, head_dim)
+    k = torch.full(shape, float("nan"), dtype=dtype)
+    v = torch.full(shape, float("nan"), dtype=dtype)
+    kf = k.view(nb * block_size, num_kv_heads, head_dim)
+    vf = v.view(nb * block_size, num_kv_heads, head_dim)
+    for tbl, ctx in zip(tables, context_lens):
+        if ctx == 0:
+            continue
+        t = torch.arange(ctx)
+        slots = torch.tensor(tbl, dtype=torch.long)[t // block_size] * block_size + t % block_size
+        kf[slots] = (torch.randn(ctx, num_kv_heads, head_dim, generator=g) * value_scale).to(dtype)
+        vf[slots] = (torch.randn(ctx, num_kv_heads, head_dim, generator=g) * value_scale).to(dtype)
+    return k, v, tables
+
+
+def padded_tables(tables, width: int | None = None) -> torch.Tensor:
+    width = width or max(len(t) for t in tables)
+    out = torch.full((len(tables), width), -1, dtype=torch.int32)
+    for i, t in enumerate(tables):
+        out[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    return out

@@ -1,0 +1,80 @@
+"""The "gpu" AttentionNode backend against the CPU oracle of
+CpuAttentionBackend, step by step, with the node's payload shapes."""
+import math
+
+import pytest
+import torch
+
+from cloverinfer_amd.attention_backend import GpuAttentionBackend, create_attention_backend
+from oracle.attention import CpuAttentionOracle
+from tests.helpers import assert_attention_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _drive(layers, hq, hkv, d, dtype, prompt_lens, steps, scale, seed, batch=True,
+           reserve=0, block_size=16):
+    g = torch.Generator().manual_seed(seed)
+    gpu = create_attention_backend("gpu", {"num_blocks": 512, "block_size": block_size})
+    cpu = CpuAttentionOracle()
+    rids = [f"req{i}" for i in range(len(prompt_lens))]
+    for rid, T in zip(rids, prompt_lens):
+        kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(T, hkv, d, generator=g).to(dtype)} for _ in range(layers)]
+        assert gpu.init_request(rid, kv, decode_reserve_tokens=reserve) == T
+        assert cpu.init_request(rid, kv) == T
+    for step in range(steps):
+        for layer in range(layers):
+            items = [{"request_id": rid, "layer_idx": layer,
+                      "query": torch.randn(1, hq, d, generator=g).to(dtype),
+                      "key": torch.randn(hkv, d, generator=g).to(dtype),
+                      "value": torch.randn(1, hkv, d, generator=g).to(dtype),
+                      "score_scale": scale} for rid in rids]
+            if batch:
+                got = gpu.decode_layer_batch(items)
+            else:
+                got = [gpu.decode_layer(it["request_id"], it["layer_idx"], it["query"],
+                                        it["key"], it["value"], it["score_scale"]) for it in items]
+            ref = cpu.decode_layer_batch(items)
+            for a, b in zip(got, ref):
+                assert a.shape == b.shape and a.dtype == b.dtype and a.device == b.device
+                assert_attention_close(a, b, what=f"step {step} layer {layer}")
+        for rid in rids:
+            assert gpu.get_context_len(rid) == cpu.get_context_len(rid)
+    return gpu, rids
+
+
+def test_opt125m_shape_fp16():
+    # OPT pre-scales q and sends score_scale 1.0 (src/core/model_adapter.py:373,386).
+    _drive(layers=12, hq=12, hkv=12, d=64, dtype=torch.float16, prompt_lens=[5, 17, 40],
+           steps=3, scale=1.0, seed=21)
+
+
+def test_qwen_gqa_shape_bf16_single_items():
+    _drive(layers=2, hq=28, hkv=4, d=128, dtype=torch.bfloat16, prompt_lens=[15, 16, 300],
+           steps=3, scale=1 / math.sqrt(128), seed=22, batch=False, block_size=8)
+
+
+def test_fp32_reserve_and_free():
+    gpu, rids = _drive(layers=2, hq=4, hkv=4, d=64, dtype=torch.float32, prompt_lens=[0, 31],
+                       steps=2, scale=0.125, seed=23, reserve=64)
+    info = gpu.get_debug_info()
+    assert info["requests"] == 2 and info["backend"] == "gpu"
+    before = info["free_blocks"]
+    gpu.free_request(rids[1])
+    gpu.free_request(rids[1])
+    assert gpu.get_debug_info()["free_blocks"] > before
+
+
+def test_protocol_errors():
+    gpu = GpuAttentionBackend(num_blocks=4, block_size=16)
+    kv = [{"key": torch.randn(3, 2, 64), "value": torch.randn(3, 2, 64)}]
+    gpu.init_request("a", kv)
+    with pytest.raises(ValueError):
+        gpu.init_request("a", kv)
+    with pytest.raises(KeyError):
+        gpu.decode_layer("b", 0, torch.randn(2, 64), torch.randn(2, 64), torch.randn(2, 64))
+    with pytest.raises(RuntimeError, match="OOM"):
+        gpu.init_request("big", [{"key": torch.randn(200, 2, 64), "value": torch.randn(200, 2, 64)}])
+    with pytest.raises(ValueError):
+        create_attention_backend("cpu")

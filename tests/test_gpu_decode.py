@@ -1,0 +1,179 @@
+"""Paged decode on the GPU against the fp32 CPU oracle, through the C ABI.
+
+Oracle-sized cases compare every output element; full-size configurations
+are checked on sampled sequences plus split-K == single-pass."""
+import math
+
+import pytest
+import torch
+
+from cloverinfer_amd import kernels
+from cloverinfer_amd.memory_manager import KVCacheManager
+from oracle import attention as oa
+from tests.helpers import assert_attention_close, make_paged_kv, padded_tables
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def run_decode(q, k, v, tables, ctx, scale, partition_size=None, width=None):
+    qg = q.to(DEV)
+    out = torch.empty_like(qg)
+    bt = padded_tables(tables, width).to(DEV)
+    cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    kernels.paged_attention(out, qg, k.to(DEV), v.to(DEV), bt, cl, k.shape[1], max(ctx),
+                            scale=scale, partition_size=partition_size)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def case(seed, ctx, hq, hkv, d, bs, dtype, scale=None, value_scale=1.0):
+    k, v, tables = make_paged_kv(seed, ctx, hkv, d, bs, dtype, value_scale, spare_blocks=3)
+    g = torch.Generator().manual_seed(seed + 1)
+    q = (torch.randn(len(ctx), hq, d, generator=g) * value_scale).to(dtype)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    return q, k, v, tables, scale
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (28, 4, 128), (32, 8, 64), (16, 1, 128),
+                                      (32, 1, 64), (6, 2, 256), (4, 4, 32)])
+@pytest.mark.parametrize("partition", [0, 32, 512])
+def test_decode_matches_oracle(dtype, hq, hkv, d, partition):
+    ctx = [1, 17, 31, 32, 33, 100, 511, 513, 1000, 0]
+    print(f"decode dtype={dtype} hq={hq} hkv={hkv} d={d} P={partition}", flush=True)
+    q, k, v, tables, scale = case(hq * 7 + d, ctx, hq, hkv, d, 16, dtype)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    assert_attention_close(got, ref, what=f"{dtype} {hq}/{hkv} d{d} P{partition}")
+    assert torch.equal(got[-1].float(), torch.zeros(hq, d))  # empty context -> zeros
+
+
+@pytest.mark.parametrize("bs", [4, 8, 32, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_block_sizes(bs, dtype):
+    ctx = [5, 64, 129, 300]
+    q, k, v, tables, scale = case(bs, ctx, 14, 2, 128, bs, dtype)
+    for partition in (0, 64):
+        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition, width=40)
+        ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+        assert_attention_close(got, ref, what=f"bs{bs} {dtype} P{partition}")
+
+
+def test_decode_strided_query_and_output():
+    ctx = [40, 200, 77]
+    q, k, v, tables, scale = case(11, ctx, 8, 2, 128, 16, torch.float16)
+    qkv = torch.randn(3, 12, 128).half().to(DEV)
+    qkv[:, :8] = q.to(DEV)
+    qv = qkv[:, :8]          # strided view (seq stride 12*128)
+    outbuf = torch.zeros(3, 10, 128, dtype=torch.float16, device=DEV)
+    out = outbuf[:, 1:9]
+    kernels.paged_attention(out, qv, k.to(DEV), v.to(DEV), padded_tables(tables).to(DEV),
+                            torch.tensor(ctx, dtype=torch.int32, device=DEV), 16, max(ctx),
+                            scale=scale)
+    torch.cuda.synchronize()
+    assert_attention_close(out.cpu(), oa.paged_decode(q, k, v, tables, ctx, scale))
+    assert torch.equal(outbuf[:, 0].cpu(), torch.zeros(3, 128, dtype=torch.float16))
+    assert torch.equal(outbuf[:, 9].cpu(), torch.zeros(3, 128, dtype=torch.float16))
+
+
+def test_decode_large_scores_and_one_hot():
+    # Peaked softmax: one key aligned with q at a large score.
+    ctx = [700]
+    q, k, v, tables, _ = case(12, ctx, 4, 4, 128, 16, torch.bfloat16)
+    t = 555
+    b, o = tables[0][t // 16], t % 16
+    k[b, o] = (q[0].float() * 4).to(torch.bfloat16)
+    got = run_decode(q, k, v, tables, ctx, 1.0 / math.sqrt(128), partition_size=64)
+    ref = oa.paged_decode(q, k, v, tables, ctx, 1.0 / math.sqrt(128))
+    assert_attention_close(got, ref)
+    assert torch.allclose(got[0].float(), v[b, o].float(), atol=2e-2)
+
+
+def test_reference_kat_test_kernels_on_gpu():
+    """tests/test_kernels.py:14-63 through the manager: every output element is
+    sum_t t e^{2 sqrt(2) t} / sum_t e^{2 sqrt(2) t} = 3.93718491..."""
+    import json, os
+    kat = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                      "reference_kats.json")))["test_kernels_append"]
+    m = KVCacheManager(16, 4, 2, 8, device=DEV)
+    m.allocate("req_1", seq_len=0)
+    for _ in range(5):
+        m.append_slot("req_1")
+    blocks = m.block_tables["req_1"]
+    for i in range(4):
+        m.k_cache[blocks[0], i] = i
+        m.v_cache[blocks[0], i] = i
+    m.k_cache[blocks[1], 0] = 4
+    m.v_cache[blocks[1], 0] = 4
+    out = m.attention(torch.ones(1, 2, 8, device=DEV), ["req_1"])
+    torch.cuda.synchronize()
+    assert out.shape == (1, 2, 8)
+    assert torch.allclose(out.cpu(), torch.full((1, 2, 8), kat["expected_output_every_element"]),
+                          atol=1e-5, rtol=0)
+
+
+def test_reference_kat_identical_rows_on_gpu():
+    """tests/verify_attention.py:88-136 asserted: 50 copies of one (k, v) give v."""
+    m = KVCacheManager(100, 16, 4, 32, dtype=torch.float16, device=DEV)
+    m.allocate("r", seq_len=0)
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(4, 32, generator=g).half().to(DEV)
+    v = torch.randn(4, 32, generator=g).half().to(DEV)
+    for _ in range(50):
+        m.write_new_kv("r", k, v)
+    assert m.block_tables["r"] == [99, 98, 97, 96]
+    q = torch.randn(1, 4, 32, generator=g).half().to(DEV)
+    out = m.attention(q, ["r"])
+    torch.cuda.synchronize()
+    assert torch.allclose(out[0].float().cpu(), v.float().cpu(), atol=1e-2, rtol=1e-2)
+
+
+# ---------------------------------------------------------------- configs
+def test_config_opt125m_fp32_with_append():
+    """8 seqs, 12 heads, D 64, fp32, 64-block pool in random order: 127 tokens
+    prefilled, one appended through reshape_and_cache -> context 128."""
+    g = torch.Generator().manual_seed(1001)
+    m = KVCacheManager(64, 16, 12, 64, dtype=torch.float32, device=DEV)
+    m.free_blocks = torch.randperm(64, generator=g).tolist()
+    rids = [f"s{i}" for i in range(8)]
+    kv = {}
+    for rid in rids:
+        kd, vd = torch.randn(128, 12, 64, generator=g), torch.randn(128, 12, 64, generator=g)
+        kv[rid] = (kd, vd)
+        m.load_initial_kv(rid, kd[:127].to(DEV), vd[:127].to(DEV))
+    m.write_new_kv_batch(rids, torch.stack([kv[r][0][127] for r in rids]).to(DEV),
+                         torch.stack([kv[r][1][127] for r in rids]).to(DEV))
+    q = torch.randn(8, 12, 64, generator=g)
+    out = m.attention(q.to(DEV), rids)
+    torch.cuda.synchronize()
+    ref = torch.stack([oa.attend(q[i], kv[r][0], kv[r][1], 1 / 8) for i, r in enumerate(rids)])
+    assert_attention_close(out.cpu(), ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("nseq", [4])
+def test_config_llama7b_mha_fp16(nseq):
+    ctx = [2048] * nseq
+    q, k, v, tables, scale = case(1002, ctx, 32, 32, 128, 16, torch.float16, value_scale=0.5)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    for partition in (0, 512):
+        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
+        assert_attention_close(got, ref, what=f"llama7b P{partition}")
+
+
+def test_config_qwen7b_gqa_bf16_ragged():
+    ctx = [int(torch.randint(256, 8193, (1,), generator=torch.Generator().manual_seed(1003000 + i)))
+           for i in range(8)]
+    q, k, v, tables, scale = case(1003, ctx, 28, 4, 128, 16, torch.bfloat16)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    for partition in (None, 0, 256, 512):
+        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
+        assert_attention_close(got, ref, what=f"qwen7b P{partition}")
+
+
+def test_config_long_context_splitk_fp16():
+    ctx = [32768, 32768]
+    q, k, v, tables, scale = case(1004, ctx, 32, 8, 128, 16, torch.float16)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=512)
+    assert_attention_close(got, ref, what="long-context P512")

@@ -1,0 +1,90 @@
+"""Chunked prefill over paged KV on the GPU: against the oracle (row i ==
+the i-th successive append-then-attend decode step) and, at the full
+8 x (4096 cached + 512 new) shape, against the GPU decode kernel run with
+each row's causal context length."""
+import math
+
+import pytest
+import torch
+
+from cloverinfer_amd import kernels
+from oracle import attention as oa
+from tests.helpers import assert_attention_close, make_paged_kv, padded_tables
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def build(seed, cached, new, hq, hkv, d, bs, dtype):
+    ctx = [c + n for c, n in zip(cached, new)]
+    k, v, tables = make_paged_kv(seed, ctx, hkv, d, bs, dtype, spare_blocks=2)
+    g = torch.Generator().manual_seed(seed + 1)
+    q = torch.randn(sum(new), hq, d, generator=g).to(dtype)
+    qsl = [0]
+    for n in new:
+        qsl.append(qsl[-1] + n)
+    return q, k, v, tables, ctx, qsl
+
+
+def run_prefill(q, k, v, tables, ctx, qsl, scale):
+    qg = q.to(DEV)
+    out = torch.full_like(qg, float("nan"))
+    kernels.chunked_prefill(out, qg, k.to(DEV), v.to(DEV), padded_tables(tables).to(DEV),
+                            torch.tensor(ctx, dtype=torch.int32, device=DEV),
+                            torch.tensor(qsl, dtype=torch.int32, device=DEV),
+                            max(b - a for a, b in zip(qsl, qsl[1:])), scale=scale)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def oracle_prefill(q, k, v, tables, ctx, qsl, scale):
+    outs = []
+    for s in range(len(ctx)):
+        kk, vv = oa.gather_context(k, v, tables[s], ctx[s])
+        outs.append(oa.chunked_prefill(q[qsl[s]:qsl[s + 1]], kk, vv, scale))
+    return torch.cat(outs)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (28, 4, 128), (4, 2, 32)])
+def test_prefill_matches_oracle(dtype, hq, hkv, d):
+    print(f"prefill dtype={dtype} hq={hq} hkv={hkv} d={d}", flush=True)
+    cached = [0, 5, 130, 300, 64]
+    new = [7, 64, 1, 100, 129]
+    q, k, v, tables, ctx, qsl = build(hq + d, cached, new, hq, hkv, d, 16, dtype)
+    scale = 1.0 / math.sqrt(d)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what=f"prefill {dtype} {hq}/{hkv} d{d}")
+
+
+def test_prefill_reduced_chunk_config():
+    """2 sequences of the chunked-prefill config (4096 cached + 512 new)."""
+    cached, new = [4096, 4096], [512, 512]
+    q, k, v, tables, ctx, qsl = build(1005, cached, new, 32, 8, 128, 16, torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what="chunked prefill 4096+512")
+
+
+def test_prefill_rows_equal_decode_steps_full_config():
+    """8 x (4096 + 512), bf16: every query row equals the decode kernel over
+    that row's causal context (the same K/V, a per-row context length)."""
+    cached, new = [4096] * 8, [512] * 8
+    q, k, v, tables, ctx, qsl = build(1006, cached, new, 32, 8, 128, 16, torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    # Decode view: one "sequence" per query row, sharing its sequence's table.
+    rows_tables, rows_ctx = [], []
+    for s in range(8):
+        for i in range(512):
+            rows_tables.append(tables[s])
+            rows_ctx.append(cached[s] + i + 1)
+    kg, vg = k.to(DEV), v.to(DEV)
+    out = torch.empty(q.shape, dtype=q.dtype, device=DEV)
+    kernels.paged_attention(out, q.to(DEV), kg, vg, padded_tables(rows_tables).to(DEV),
+                            torch.tensor(rows_ctx, dtype=torch.int32, device=DEV), 16,
+                            max(rows_ctx), scale=scale, partition_size=0)
+    torch.cuda.synchronize()
+    assert_attention_close(got, out.cpu(), what="prefill rows vs decode")

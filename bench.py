@@ -343,13 +343,38 @@ def bench_prefill(args):
     }
 
 
+def bench_copy(args):
+    """Calibration workload: a plain device copy of a known number of bytes
+    (2 GiB read + 2 GiB written per step), used to scale HBM byte counters."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    n = 1 << 31
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    return {"metric": "device copy GB/s (read + write)", "value": 2 * n / (ms * 1e-3) / 1e9,
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "u8", "data": "constant bytes",
+            "config": {"workload": "calibration copy, 2 GiB read + 2 GiB write per step",
+                       "bytes_read_per_step": n, "bytes_written_per_step": n}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen7b",
-                    choices=sorted(DECODE_CONFIGS) + ["prefill"])
+                    choices=sorted(DECODE_CONFIGS) + ["prefill", "copy"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass; default: automatic)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -368,6 +393,8 @@ def main() -> int:
         return 1
     if args.config == "prefill":
         result = bench_prefill(args)
+    elif args.config == "copy":
+        result = bench_copy(args)
     else:
         result = bench_decode(args, DECODE_CONFIGS[args.config])
     print(json.dumps(result), flush=True)

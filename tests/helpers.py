@@ -5,12 +5,14 @@ import math
 
 import torch
 
-# Parity bar for attention outputs against the fp32 oracle: max-abs 2e-3, and
-# 1e-2 relative where the reference value is at least 0.2 in magnitude (a pure
-# relative bound on near-zero 16-bit outputs is ill-posed).
+# Parity bar for attention outputs against the fp32 oracle, elementwise
+#     |got - ref| <= ATOL + RTOL * |ref|      (ATOL = 2e-3, RTOL = 1e-2)
+# i.e. max-abs 2e-3 near zero and max-rel 1e-2 elsewhere. A pure max-abs
+# bound cannot hold for 16-bit outputs: rounding a bf16 value in [2, 4) to the
+# output dtype alone moves it by up to 2^-7 = 7.8e-3 (the reference
+# CpuAttentionBackend rounds its fp32 result to the query dtype the same way).
 ATOL = 2e-3
 RTOL = 1e-2
-REL_FLOOR = 0.2
 
 
 def assert_attention_close(got: torch.Tensor, ref: torch.Tensor, atol: float = ATOL,
@@ -19,12 +21,17 @@ def assert_attention_close(got: torch.Tensor, ref: torch.Tensor, atol: float = A
     ref = ref.detach().float().cpu()
     assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} != {tuple(ref.shape)}"
     assert torch.isfinite(got).all(), f"{what}: non-finite output"
+    if not got.numel():
+        return
     err = (got - ref).abs()
-    max_abs = err.max().item() if err.numel() else 0.0
-    big = ref.abs() >= REL_FLOOR
-    max_rel = (err[big] / ref.abs()[big]).max().item() if big.any() else 0.0
-    assert max_abs <= atol, f"{what}: max-abs {max_abs:.3e} > {atol:.1e}"
-    assert max_rel <= rtol, f"{what}: max-rel {max_rel:.3e} > {rtol:.1e}"
+    bound = atol + rtol * ref.abs()
+    bad = err > bound
+    if bad.any():
+        i = int(torch.argmax((err - bound).flatten()))
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {err.numel()} elements outside {atol:g} + {rtol:g}*|ref|; "
+            f"worst got {got.flatten()[i].item():.6f} ref {ref.flatten()[i].item():.6f}; "
+            f"max-abs {err.max().item():.3e}")
 
 
 def make_paged_kv(seed: int, context_lens, num_kv_heads: int, head_dim: int, block_size: int,

@@ -55,7 +55,8 @@ def test_decode_block_sizes(bs, dtype):
     ctx = [5, 64, 129, 300]
     q, k, v, tables, scale = case(bs, ctx, 14, 2, 128, bs, dtype)
     for partition in (0, 64):
-        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition, width=40)
+        width = max(len(t) for t in tables) + 3  # extra -1 padding columns
+        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition, width=width)
         ref = oa.paged_decode(q, k, v, tables, ctx, scale)
         assert_attention_close(got, ref, what=f"bs{bs} {dtype} P{partition}")
 

@@ -71,6 +71,40 @@ template <> struct Mfma16x16x32<_Float16> {
   }
 };
 
+// v_mfma_f32_16x16x16_{bf16,f16}. Operand layout for lane l:
+//   A (16 x 16): row l%16, k = 4*(l/16) .. +4
+//   B (16 x 16): col l%16, k = 4*(l/16) .. +4
+//   C/D (16 x 16): col l%16, rows 4*(l/16) .. +4
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma16x16x16;
+
+template <> struct Mfma16x16x16<__bf16> {
+  typedef bf16x4 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                      __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
+};
+
+template <> struct Mfma16x16x16<_Float16> {
+  typedef f16x4 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Pack 4 fp32 values into a 4-element 16-bit MFMA operand (round to nearest even).
+template <typename T>
+__device__ __forceinline__ typename Mfma16x16x16<T>::op_t pack4(const float (&x)[4]) {
+  typename Mfma16x16x16<T>::op_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = (T)x[i];
+  return r;
+}
+
 // v_mfma_f32_32x32x16_{bf16,f16} (gfx950). Operand layout for lane l:
 //   A (32 x 16): row l%32, k = 8*(l/32) .. +8
 //   B (16 x 32): col l%32, k = 8*(l/32) .. +8
@@ -124,6 +158,27 @@ __device__ __forceinline__ V load_vec(const void *p) {
 template <typename V>
 __device__ __forceinline__ void store_vec(void *p, V v) {
   *reinterpret_cast<V *>(p) = v;
+}
+
+// Raw buffer loads: a wave-uniform base in a buffer resource (SGPRs) plus a
+// 32-bit per-lane byte offset, so the hot loops keep no 64-bit per-lane
+// addresses. The range check (num_records) is set out of the way; callers
+// keep every offset inside their allocation.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+
+template <typename V> __device__ __forceinline__ V buf_load(rsrc_t r, uint32_t off);
+
+template <> __device__ __forceinline__ u32x4 buf_load<u32x4>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+template <> __device__ __forceinline__ u32x2 buf_load<u32x2>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
 }
 
 }  // namespace clv

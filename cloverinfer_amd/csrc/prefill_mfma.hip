@@ -9,7 +9,7 @@
 // LDS serves every query head of the group. Each wave owns 32 rows (two
 // 16-row MFMA tiles). Per 64-token KV tile a wave runs
 //   S^T[t, r] = K[t, :] . Q[r, :]    4 token tiles x 2 row tiles x D/32 MFMAs
-//   O[r, d]  += P[r, t] V[t, d]      2 token halves x 2 row tiles x D/16 MFMAs
+//   O[r, d]  += P[r, t] V[t, d]      2 token halves x 2 row tiles x 2 x D/16 MFMAs
 // (v_mfma_f32_16x16x32_{bf16,f16}), with an fp32 online softmax between.
 // As in the decode kernel, each lane's P values are already its A operand
 // of the PV product, and V is regrouped from 16-byte row chunks with v_perm.
@@ -216,15 +216,20 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
           vr[4 * h + r] = load_vec<vchunk_t>(&V[(32 * half + 16 * h + 4 * j + r) * LROW + n16 * CH]);
-      op_t pa[2];
+      // P split into its 16-bit value and the 16-bit rounding residual, so
+      // that P.V keeps fp32-level accuracy.
+      op_t pa[2], pl[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        float x[8];
+        float x[8], lo[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int r = 0; r < 4; ++r) x[4 * h + r] = pf[rt][4 * (2 * half + h) + r];
         pa[rt] = pack8<T>(x);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) lo[k] = x[k] - (float)pa[rt][k];
+        pl[rt] = pack8<T>(lo);
       }
 #pragma unroll
       for (int m = 0; m < CH; ++m) {
@@ -238,6 +243,8 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
         const op_t vb = __builtin_bit_cast(op_t, w);
         o[0][m] = Mf::run(pa[0], vb, o[0][m]);
         o[1][m] = Mf::run(pa[1], vb, o[1][m]);
+        o[0][m] = Mf::run(pl[0], vb, o[0][m]);
+        o[1][m] = Mf::run(pl[1], vb, o[1][m]);
       }
     }
 

@@ -5,7 +5,7 @@ Default workload (the headline metric): paged decode at the GQA
 Qwen2.5-7B shape - 128 sequences, 28 query / 4 kv heads, head_dim 128,
 block 16, bf16, context lengths uniform in [256, 8192] (seeded per
 sequence), pool sized to the tokens + 10 %, blocks scattered at random.
-A step is one decode pass over the batch (split-K partials + LSE merge).
+A step is one decode pass over the batch (balanced stream decode + LSE merge).
 Inputs are resident in HBM before the timed region.
 
 Prints one JSON line (stdout) with the whole-job throughput in GB/s of
@@ -167,26 +167,48 @@ def bench_decode(args, cfg):
     w = decode_workload(cfg, dev)
     out = torch.empty_like(w["q"])
     max_ctx = max(w["ctx"])
-    part = args.partition if args.partition is not None else cfg["partition"]
-    if part is None:
-        hq, hkv = cfg["hq"], cfg["hkv"]
-        part = kernels.choose_partition(len(w["ctx"]), hkv, hq // hkv, max_ctx,
-                                        kernels.num_compute_units(dev))
     a = kernels.decode_args(out, w["q"], w["k"], w["v"], w["table"], w["ctx_dev"], w["bs"],
                             max_ctx, scale=w["scale"])
-    split = part > 0 and max_ctx > part
+    part = args.partition if args.partition is not None else cfg["partition"]
+    if part is None:
+        if kernels.balanced_supported(a):
+            mode = "balanced"
+        else:
+            hq, hkv = cfg["hq"], cfg["hkv"]
+            part = kernels.choose_partition(len(w["ctx"]), hkv, hq // hkv, max_ctx,
+                                            kernels.num_compute_units(dev))
+            mode = "split" if part > 0 and max_ctx > part else "single"
+    else:
+        mode = "split" if part > 0 and max_ctx > part else "single"
     stream = torch.cuda.current_stream(dev)
-    ws = kernels.splitk_workspace(dev, kernels.workspace_bytes(a, part)) if split else None
     lib = kernels._native.load()
+    waves = args.waves
+    if mode == "balanced":
+        ws = kernels.splitk_workspace(dev, kernels.balanced_workspace_bytes(a, waves))
+    elif mode == "split":
+        ws = kernels.splitk_workspace(dev, kernels.workspace_bytes(a, part))
+    else:
+        ws = None
 
-    def step():
-        if split:
+    def first_half():
+        if mode == "balanced":
+            kernels.balanced_partials(a, waves, ws, stream.cuda_stream)
+        elif mode == "split":
             kernels.paged_decode_partials(a, part, ws, stream.cuda_stream)
-            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
         else:
             kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
 
-    log(f"warmup {args.warmup} (partition {part if split else 0})")
+    def second_half():
+        if mode == "balanced":
+            kernels.balanced_reduce(a, waves, ws, stream.cuda_stream)
+        elif mode == "split":
+            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
+
+    def step():
+        first_half()
+        second_half()
+
+    log(f"warmup {args.warmup} (mode {mode}, partition {part if mode == 'split' else 0})")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -198,17 +220,16 @@ def bench_decode(args, cfg):
     wall = time.perf_counter() - t0
     ms = wall / args.steps * 1e3
 
-    # Per-kernel durations: HIP events on the stream the kernels run on.
+    # Per-kernel durations: HIP events on the stream the kernels run on. A
+    # leading device-side sleep keeps the GPU busy while every launch is
+    # queued, so host launch gaps stay out of the event intervals.
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda._sleep(50_000_000)
     for e in ev:
         e[0].record(stream)
-        if split:
-            kernels.paged_decode_partials(a, part, ws, stream.cuda_stream)
-            e[1].record(stream)
-            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
-        else:
-            kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
-            e[1].record(stream)
+        first_half()
+        e[1].record(stream)
+        second_half()
         e[2].record(stream)
     torch.cuda.synchronize()
     dec_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
@@ -244,16 +265,19 @@ def bench_decode(args, cfg):
             "block_size": w["bs"],
             "total_context_tokens": sum(w["ctx"]),
             "max_context_len": max_ctx,
-            "partition_size": part if split else 0,
+            "schedule": mode,
+            "partition_size": part if mode == "split" else 0,
             "algorithmic_bytes_per_step": w["algo_bytes"],
             "seed": cfg["seed"],
         },
         "tokens_per_s": len(w["ctx"]) / (ms * 1e-3),
         "hbm_frac_of_peak": value / PEAK_HBM_GBS,
-        "kernels_us": {"paged_decode": dec_us, "splitk_reduce": red_us if split else 0.0},
+        "kernels_us": {"paged_decode": dec_us, "merge": red_us},
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_decode_mfma" if cfg["dtype"] != "float32" else "paged_decode_valu",
+            "kernel": {"balanced": "paged_decode_stream", "split": "paged_decode_mfma",
+                       "single": "paged_decode_mfma"}[mode] if cfg["dtype"] != "float32"
+                      else "paged_decode_valu",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
@@ -377,6 +401,8 @@ def main() -> int:
                     choices=sorted(DECODE_CONFIGS) + ["prefill", "copy"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass; default: automatic)")
+    ap.add_argument("--waves", type=int, default=0,
+                    help="waves of the balanced decode (0 = device default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU baseline work (a bounded sample)")

@@ -28,6 +28,7 @@ SOURCES = [
     "clover_attn_abi.hip",
     "cache_ops.hip",
     "decode.hip",
+    "decode_stream.hip",
     "prefill.hip",
     "prefill_mfma.hip",
 ]

@@ -234,6 +234,93 @@ int clv_paged_decode_splitk(const clv_decode_args *a, int32_t partition_size, vo
   return clv_splitk_reduce(a, partition_size, workspace, workspace_bytes, stream);
 }
 
+int32_t clv_default_num_waves(void) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 2048;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 2048;
+  // Two 4-wave workgroups per compute unit: the decode kernel's occupancy.
+  return cus * 8;
+}
+
+size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t num_waves) {
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      num_heads % num_kv_heads != 0)
+    return 0;
+  if (num_waves <= 0) num_waves = clv_default_num_waves();
+  const int64_t group = num_heads / num_kv_heads;
+  const size_t nseg = (size_t)num_seqs * (size_t)num_kv_heads * (size_t)ceil_div(group, 16);
+  const size_t rows = ((size_t)num_waves + nseg) * 16;
+  return 2 * round256((nseg + 1) * 4) + 2 * round256(rows * 4) + round256(rows * (size_t)head_dim * 4);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Validates a balanced-decode call and lays the workspace out in p.
+int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
+                  size_t workspace_bytes, clv::DecodeParams *p) {
+  const int st = fill_decode(a, p);
+  if (st != CLV_OK) return st;
+  if (num_waves <= 0) num_waves = clv_default_num_waves();
+  if (num_waves > (1 << 22)) return CLV_EINVAL;
+  const int64_t nseg = (int64_t)p->num_seqs * p->num_kv_heads * p->n_gchunks;
+  if (!clv::decode_stream_supported((DType)a->dtype, a->head_dim, a->block_size, nseg))
+    return CLV_EUNSUPPORTED;
+  if (p->num_seqs == 0) return CLV_OK;
+  const size_t need = clv_balanced_workspace_bytes(a->num_seqs, a->num_heads, a->num_kv_heads,
+                                                   a->head_dim, num_waves);
+  if (workspace == nullptr || workspace_bytes < need || ((uintptr_t)workspace & 255u) != 0)
+    return CLV_EWORKSPACE;
+  const size_t rows = ((size_t)num_waves + (size_t)nseg) * 16;
+  char *ws = (char *)workspace;
+  p->num_waves = num_waves;
+  p->num_segments = (int32_t)nseg;
+  p->seg_prefix = (int32_t *)ws;
+  ws += round256(((size_t)nseg + 1) * 4);
+  p->slot_prefix = (int32_t *)ws;
+  ws += round256(((size_t)nseg + 1) * 4);
+  p->ws_m = (float *)ws;
+  ws += round256(rows * 4);
+  p->ws_l = (float *)ws;
+  ws += round256(rows * 4);
+  p->ws_o = (float *)ws;
+  return CLV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int clv_balanced_partials(const clv_decode_args *a, int32_t num_waves, void *workspace,
+                          size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_balanced(a, num_waves, workspace, workspace_bytes, &p);
+  if (st != CLV_OK || p.num_seqs == 0) return st;
+  return clv::launch_decode_stream(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
+}
+
+int clv_balanced_reduce(const clv_decode_args *a, int32_t num_waves, const void *workspace,
+                        size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_balanced(a, num_waves, const_cast<void *>(workspace), workspace_bytes, &p);
+  if (st != CLV_OK || p.num_seqs == 0) return st;
+  return clv::launch_stream_reduce(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
+}
+
+int clv_paged_decode_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
+                              size_t workspace_bytes, clv_stream_t stream) {
+  const int rc = clv_balanced_partials(a, num_waves, workspace, workspace_bytes, stream);
+  if (rc != CLV_OK) return rc;
+  return clv_balanced_reduce(a, num_waves, workspace, workspace_bytes, stream);
+}
+
 int clv_chunked_prefill(const clv_prefill_args *a, clv_stream_t stream) {
   if (a == nullptr) return CLV_EINVAL;
   if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;

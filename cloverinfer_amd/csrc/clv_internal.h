@@ -30,7 +30,18 @@ struct DecodeParams {
   float *ws_o;            // [num_seqs, num_heads, max_parts, head_dim] normalised contexts
   float *ws_m;            // [num_seqs, num_heads, max_parts] row max (natural-log domain)
   float *ws_l;            // [num_seqs, num_heads, max_parts] row sum
+  // Balanced (stream) mode: num_waves waves split the flattened
+  // (sequence, kv head, query-head chunk, 16-token step) space evenly; the
+  // workspace holds one partial per (segment, wave) pair, 16 rows each, in
+  // ws_o/ws_m/ws_l, plus the segment prefix sums written by workgroup 0.
+  int32_t num_waves;
+  int32_t num_segments;   // num_seqs * num_kv_heads * n_gchunks
+  int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
+  int32_t *slot_prefix;   // [num_segments + 1] exclusive prefix of partials per segment
 };
+
+// Largest segment count the balanced mode keeps in LDS.
+constexpr int kStreamMaxSegments = 4096;
 
 struct CacheParams {
   const void *key;
@@ -69,11 +80,14 @@ hipError_t launch_reshape_and_cache(const CacheParams &p, hipStream_t stream);
 hipError_t launch_decode_mfma(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_decode_valu(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_splitk_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
+hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream);
+hipError_t launch_stream_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream);
 hipError_t launch_prefill_valu(const PrefillParams &p, DType dt, hipStream_t stream);
 
 // Whether the MFMA decode kernel covers this shape/dtype.
 bool decode_mfma_supported(DType dt, int head_dim, int block_size);
+bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments);
 bool prefill_mfma_supported(DType dt, int head_dim, int block_size);
 
 }  // namespace clv

@@ -24,19 +24,12 @@
 // the B operand: no LDS round trip on the hot loop.
 // fp32 (and shapes MFMA does not cover) use a VALU kernel with the same
 // decomposition and the same epilogue.
-#include "attn_common.h"
+#include "decode_mfma.h"
 
 namespace clv {
 namespace {
 
 constexpr int kStep = 32;  // tokens per wave step in the MFMA kernel
-
-// Clamp a context length to what the grid and the block table cover.
-__device__ __forceinline__ int clamp_ctx(const DecodeParams &p, int s) {
-  int ctx = p.context_lens[s];
-  const int cap = min(p.max_context_len, p.max_blocks_per_seq << p.block_shift);
-  return max(0, min(ctx, cap));
-}
 
 template <typename T>
 __device__ __forceinline__ KvView kv_view(const DecodeParams &p, int s, int kvh) {
@@ -65,51 +58,17 @@ __device__ __forceinline__ OutDesc<T> out_desc(const DecodeParams &p, int s, int
   return od;
 }
 
-template <int CH> struct VChunk;
-template <> struct VChunk<8> { typedef u32x4 type; };  // D = 128: 16 bytes
-template <> struct VChunk<4> { typedef u32x2 type; };  // D = 64: 8 bytes
-
 // ---------------------------------------------------------------- MFMA kernel
-// Loads of one 16-token step: the K rows (A operands of S^T = K Q^T, lane
-// row n16) and the V rows of the 4 tokens 4j..4j+3 whose P values the lane
-// holds (B operands of O += P V).
-template <int NQK, typename vchunk_t>
-struct StepRegs {
-  u32x4 k[NQK];
-  vchunk_t v[4];
-  bool ok;  // this lane's V rows lie in a readable block
-};
-
-// Per 16-token step a wave runs D/32 MFMAs 16x16x32 for the scores
-//   S^T[t, g] = K[t, :] . Q[g, :]     (lane holds S[g = n16][t = 4j + r])
-// and 2 x D/16 MFMAs 16x16x16 for O[g, d] += P[g, t] V[t, d], whose A operand
-// is exactly the lane's 4 P values (P split into a 16-bit high part and its
-// rounding residual, so P.V keeps fp32-level accuracy) and whose B operand
-// for output column block m is element m of the lane's 4 V row chunks,
-// regrouped with v_perm. Loads of the next step are in flight while the
-// current one is computed (two register sets).
-// UNI: block_size >= 16, so each step sits in one block and its block-table
-// entry is wave-uniform (scalar load). Otherwise (block_size 4 or 8) lanes
-// look up their own rows.
+// One workgroup (NW waves) per (sequence, kv head, 16-row query chunk,
+// partition); wave w takes the partition's 16-token steps w, w + NW, ...
+// with the loads of its next step in flight while the current one is
+// computed (two register sets), and the waves' partials are merged in LDS.
 template <typename T, int D, int NW, bool UNI>
 __global__ void __launch_bounds__(NW * 64) paged_decode_mfma(const DecodeParams p) {
-  typedef Mfma16x16x32<T> MfK;
-  typedef Mfma16x16x16<T> MfV;
-  typedef typename MfK::op_t qk_t;
-  typedef typename MfV::op_t pv_t;
-  constexpr int NQK = D / 32;  // QK MFMAs per step
-  constexpr int CH = D / 16;   // V elements per lane per token = PV output blocks
-  constexpr int EB = (int)sizeof(T);
-  constexpr int STEP = 16;
-  typedef typename VChunk<CH>::type vchunk_t;
-  typedef StepRegs<NQK, vchunk_t> Regs;
-
+  typedef DecodeWave<T, D, UNI> W;
   __shared__ WaveSmem<NW, 16, D> sm;
 
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n16 = lane & 15;
-  const int j = lane >> 4;
   const int s = blockIdx.z;
   const int kvh = blockIdx.y / p.n_gchunks;
   const int g0 = (blockIdx.y - kvh * p.n_gchunks) * 16;
@@ -124,165 +83,46 @@ __global__ void __launch_bounds__(NW * 64) paged_decode_mfma(const DecodeParams 
     t_end = min(ctx, t_begin + p.partition_size);
   }
 
-  // Q as the B operand of S^T = K Q^T: lane holds Q[g = n16][d = 32i + 8j .. +8].
-  qk_t qop[NQK];
-  {
-    const T *qrow = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)(h0 + n16) * p.q_stride_head;
-#pragma unroll
-    for (int i = 0; i < NQK; ++i) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (n16 < ng) w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
-      qop[i] = __builtin_bit_cast(qk_t, w);
-    }
-  }
-
-  const int32_t *bt = p.block_tables + (int64_t)s * p.max_blocks_per_seq;
-  const char *kbase = (const char *)p.k_cache + (int64_t)kvh * p.kv_stride_head * EB;
-  const char *vbase = (const char *)p.v_cache + (int64_t)kvh * p.kv_stride_head * EB;
-  const int64_t sblk = p.kv_stride_block * EB;
-  const int64_t stok = p.kv_stride_token * EB;
-  const int bshift = p.block_shift;
-  const int bmask = (1 << bshift) - 1;
-  const unsigned nblocks = (unsigned)p.num_blocks;
-  // Lane offsets inside a step (bytes, below 16 rows of the token stride):
-  // K row n16 at d = 8j (+32 elements per MFMA), V rows 4j + r at d = n16*CH.
-  const uint32_t k_lane = (uint32_t)(n16 * stok + 8 * j * EB);
-  uint32_t v_lane[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) v_lane[r] = (uint32_t)((4 * j + r) * stok + n16 * CH * EB);
-
-  // Issue every load of the step starting at token `base` (< t_end). All
-  // addresses are in bounds: rows past t_end or in unreadable blocks read a
-  // readable row and are masked when the step is computed.
-  auto issue = [&](int base, Regs &R) {
-    if constexpr (UNI) {
-      // Wave-uniform block: scalar base address plus 32-bit lane offsets.
-      const int blk = bt[base >> bshift];
-      const bool ok = (unsigned)blk < nblocks;
-      const int64_t off = ok ? blk * sblk + (base & bmask) * stok : 0;
-      R.ok = ok;
-      const rsrc_t rk = make_rsrc(kbase + off);
-      const rsrc_t rv = make_rsrc(vbase + off);
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4>(rk, k_lane + 64u * i);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t>(rv, v_lane[r]);
-    } else {
-      const int tk = base + n16;
-      const int kb = tk < t_end ? bt[tk >> bshift] : 0;
-      const bool kok = tk < t_end && (unsigned)kb < nblocks;
-      const int64_t koff = (kok ? kb * sblk + (tk & bmask) * stok : 0) + 8 * j * EB;
-      const int tv = base + 4 * j;
-      const int vb = tv < t_end ? bt[tv >> bshift] : 0;
-      const bool vok = tv < t_end && (unsigned)vb < nblocks;
-      R.ok = vok;
-      const int64_t voff = (vok ? vb * sblk + (tv & bmask) * stok : 0) + n16 * CH * EB;
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) R.k[i] = load_vec<u32x4>(kbase + koff + 64 * i);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) R.v[r] = load_vec<vchunk_t>(vbase + voff + r * stok);
-    }
-  };
-
-  f32x4 o[CH];
-#pragma unroll
-  for (int m = 0; m < CH; ++m) o[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;  // running max for row g = n16 (log2 domain)
-  float l_run = 0.f;      // this lane's share of the row sum
-
-  auto compute = [&](int base, Regs &R) {
-    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NQK; ++i) sacc = MfK::run(__builtin_bit_cast(qk_t, R.k[i]), qop[i], sacc);
-    // Masking is needed only on a partial step or an unreadable block.
-    const bool full = __all(base + STEP <= t_end && R.ok);
-    float x[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = full || (R.ok && base + 4 * j + r < t_end);
-      x[r] = ok ? sacc[r] * p.scale_log2 : kNegInf;
-    }
-    if (!full) {
-      const vchunk_t z = {};
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (x[r] == kNegInf) R.v[r] = z;  // keep NaN/Inf of unused slots out of P.V
-    }
-    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float msub = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_run - msub);
-    float pf[4], lo[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(x[r] - msub);
-    l_run = l_run * alpha + ((pf[0] + pf[1]) + (pf[2] + pf[3]));
-    m_run = m_new;
-
-    // Rescale the accumulator rows g' = 4j + r by alpha of row g'.
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float a = shfl(alpha, 4 * j + r);
-#pragma unroll
-        for (int m = 0; m < CH; ++m) o[m][r] *= a;
-      }
-    }
-
-    const pv_t pa = pack4<T>(pf);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lo[r] = pf[r] - (float)pa[r];
-    const pv_t pl = pack4<T>(lo);
-#pragma unroll
-    for (int m = 0; m < CH; ++m) {
-      const uint32_t w0 = (m & 1) ? pair_hi(R.v[0][m >> 1], R.v[1][m >> 1])
-                                  : pair_lo(R.v[0][m >> 1], R.v[1][m >> 1]);
-      const uint32_t w1 = (m & 1) ? pair_hi(R.v[2][m >> 1], R.v[3][m >> 1])
-                                  : pair_lo(R.v[2][m >> 1], R.v[3][m >> 1]);
-      const u32x2 w = {w0, w1};
-      const pv_t vb = __builtin_bit_cast(pv_t, w);
-      o[m] = MfV::run(pa, vb, o[m]);
-      o[m] = MfV::run(pl, vb, o[m]);
-    }
-  };
+  W w;
+  w.init(p);
+  typename W::qk_t qop[W::NQK];
+  w.load_q(p, s, h0, ng, qop);
+  const SegGeom geo = seg_geom<T>(p, s, kvh, t_end);
 
   // The prefetch is unconditional (a branch around it makes the compiler wait
   // for every outstanding load): past the wave's last step it re-reads that
   // step's rows, which are still in cache, and the data is never used.
-  const int stride = NW * STEP;
-  const int first = t_begin + wave * STEP;
+  const int stride = NW * W::STEP;
+  const int first = t_begin + wave * W::STEP;
   if (first < t_end) {
     const int last = first + ((t_end - 1 - first) / stride) * stride;
     int base = first;
-    Regs A, B;
-    issue(base, A);
+    typename W::Regs A, B;
+    w.issue(geo, base, A);
     for (;;) {
-      issue(min(base + stride, last), B);
-      compute(base, A);
+      w.issue(geo, min(base + stride, last), B);
+      w.compute(base, t_end, A, qop);
       base += stride;
       if (base > last) break;
-      issue(min(base + stride, last), A);
-      compute(base, B);
+      w.issue(geo, min(base + stride, last), A);
+      w.compute(base, t_end, B, qop);
       base += stride;
       if (base > last) break;
     }
   }
 
-  // Row sums: add the four lane groups holding the same row.
-  l_run += shfl_xor(l_run, 16);
-  l_run += shfl_xor(l_run, 32);
-  if (j == 0) {
-    sm.m[wave][n16] = m_run;
-    sm.l[wave][n16] = l_run;
+  w.reduce_rowsum();
+  if (w.j == 0) {
+    sm.m[wave][w.n16] = w.m_run;
+    sm.l[wave][w.n16] = w.l_run;
   }
   // Lane holds O[g = 4j + r][d = n16*CH + m].
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float *dst = &sm.o[wave][4 * j + r][n16 * CH];
+    float *dst = &sm.o[wave][4 * w.j + r][w.n16 * W::CH];
 #pragma unroll
-    for (int m = 0; m < CH; m += 4) {
-      f32x4 v = {o[m][r], o[m + 1][r], o[m + 2][r], o[m + 3][r]};
+    for (int m = 0; m < W::CH; m += 4) {
+      f32x4 v = {w.o[m][r], w.o[m + 1][r], w.o[m + 2][r], w.o[m + 3][r]};
       store_vec<f32x4>(dst + m, v);
     }
   }

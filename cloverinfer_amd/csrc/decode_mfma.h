@@ -1,0 +1,241 @@
+// decode_mfma.h - the per-wave MFMA decode machinery shared by the grid
+// kernel (one workgroup per sequence/kv head/partition, decode.hip) and the
+// balanced stream kernel (decode_stream.hip).
+//
+// A wave attends up to 16 query rows (the query heads of one kv head, or a
+// 16-row chunk of them) over 16-token steps of one sequence's paged context.
+// Per step it runs D/32 MFMAs 16x16x32 for the scores
+//   S^T[t, g] = K[t, :] . Q[g, :]       (lane holds S[g = n16][t = 4j + r])
+// and 2 x D/16 MFMAs 16x16x16 for O[g, d] += P[g, t] V[t, d]. The A operand
+// of the second product is exactly the lane's 4 P values (split into a
+// 16-bit value and its 16-bit rounding residual, so P.V keeps fp32-level
+// accuracy); its B operand for output column block m is element m of the
+// lane's 4 V row chunks, regrouped with v_perm. Loads go through buffer
+// resources: a wave-uniform base (SGPRs) plus 32-bit lane offsets.
+#pragma once
+
+#include "attn_common.h"
+
+namespace clv {
+
+template <int CH> struct VChunk;
+template <> struct VChunk<8> { typedef u32x4 type; };  // D = 128: 16 bytes per lane
+template <> struct VChunk<4> { typedef u32x2 type; };  // D = 64: 8 bytes per lane
+
+// Clamp a context length to what the grid and the block table cover.
+__device__ __forceinline__ int clamp_ctx(const DecodeParams &p, int s) {
+  const int ctx = p.context_lens[s];
+  const int cap = min(p.max_context_len, p.max_blocks_per_seq << p.block_shift);
+  return max(0, min(ctx, cap));
+}
+
+// Where one (sequence, kv head) lives: its block-table row and pool bases.
+struct SegGeom {
+  const int32_t *bt;
+  const char *kbase;
+  const char *vbase;
+  int t_end;  // tokens [.., t_end) are attended
+};
+
+template <typename T>
+__device__ __forceinline__ SegGeom seg_geom(const DecodeParams &p, int s, int kvh, int t_end) {
+  SegGeom g;
+  g.bt = p.block_tables + (int64_t)s * p.max_blocks_per_seq;
+  g.kbase = (const char *)p.k_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
+  g.vbase = (const char *)p.v_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
+  g.t_end = t_end;
+  return g;
+}
+
+// UNI: block_size >= 16, so a step sits in one block and its block-table
+// entry is wave-uniform (scalar load, buffer loads). Otherwise (block_size 4
+// or 8) lanes look up their own rows.
+template <typename T, int D, bool UNI>
+struct DecodeWave {
+  typedef Mfma16x16x32<T> MfK;
+  typedef Mfma16x16x16<T> MfV;
+  typedef typename MfK::op_t qk_t;
+  typedef typename MfV::op_t pv_t;
+  static constexpr int NQK = D / 32;  // QK MFMAs per step
+  static constexpr int CH = D / 16;   // V elements per lane per token = PV output blocks
+  static constexpr int EB = (int)sizeof(T);
+  static constexpr int STEP = 16;
+  typedef typename VChunk<CH>::type vchunk_t;
+
+  // Loads of one step: K rows (lane row n16) and the V rows 4j..4j+3.
+  struct Regs {
+    u32x4 k[NQK];
+    vchunk_t v[4];
+    bool ok;  // the lane's V rows lie in a readable block
+  };
+
+  int n16, j;
+  int64_t sblk, stok;
+  int bshift, bmask;
+  unsigned nblocks;
+  float scale_log2;
+  uint32_t k_lane;     // byte offset of K row n16, d = 8j, inside a step
+  uint32_t v_lane[4];  // byte offsets of V rows 4j + r, d = n16 * CH
+  f32x4 o[CH];         // O[g = 4j + r][d = n16 * CH + m]
+  float m_run;         // running max of row g = n16 (log2 domain)
+  float l_run;         // this lane's share of the row sum
+
+  __device__ __forceinline__ void init(const DecodeParams &p) {
+    const int lane = threadIdx.x & 63;
+    n16 = lane & 15;
+    j = lane >> 4;
+    sblk = p.kv_stride_block * EB;
+    stok = p.kv_stride_token * EB;
+    bshift = p.block_shift;
+    bmask = (1 << bshift) - 1;
+    nblocks = (unsigned)p.num_blocks;
+    scale_log2 = p.scale_log2;
+    k_lane = (uint32_t)(n16 * stok + 8 * j * EB);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v_lane[r] = (uint32_t)((4 * j + r) * stok + n16 * CH * EB);
+    reset();
+  }
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int m = 0; m < CH; ++m) o[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    m_run = kNegInf;
+    l_run = 0.f;
+  }
+
+  // Q rows h0 .. h0+ng-1 of sequence s as the B operand of S^T = K Q^T:
+  // lane holds Q[g = n16][d = 32i + 8j .. +8] (zero for g >= ng).
+  __device__ __forceinline__ void load_q(const DecodeParams &p, int s, int h0, int ng,
+                                         qk_t (&q)[NQK]) const {
+    const T *qrow = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)(h0 + n16) * p.q_stride_head;
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (n16 < ng) w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
+      q[i] = __builtin_bit_cast(qk_t, w);
+    }
+  }
+
+  // Issue every load of the step starting at token `base` (< g.t_end). All
+  // addresses are in bounds: rows past t_end or in unreadable blocks read a
+  // readable row and are masked when the step is computed.
+  __device__ __forceinline__ void issue(const SegGeom &g, int base, Regs &R) const {
+    if constexpr (UNI) {
+      const int blk = g.bt[base >> bshift];
+      const bool ok = (unsigned)blk < nblocks;
+      const int64_t off = ok ? blk * sblk + (base & bmask) * stok : 0;
+      R.ok = ok;
+      const rsrc_t rk = make_rsrc(g.kbase + off);
+      const rsrc_t rv = make_rsrc(g.vbase + off);
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4>(rk, k_lane + 64u * i);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t>(rv, v_lane[r]);
+    } else {
+      const int tk = base + n16;
+      const int kb = tk < g.t_end ? g.bt[tk >> bshift] : 0;
+      const bool kok = tk < g.t_end && (unsigned)kb < nblocks;
+      const int64_t koff = (kok ? kb * sblk + (tk & bmask) * stok : 0) + 8 * j * EB;
+      const int tv = base + 4 * j;
+      const int vb = tv < g.t_end ? g.bt[tv >> bshift] : 0;
+      const bool vok = tv < g.t_end && (unsigned)vb < nblocks;
+      R.ok = vok;
+      const int64_t voff = (vok ? vb * sblk + (tv & bmask) * stok : 0) + n16 * CH * EB;
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) R.k[i] = load_vec<u32x4>(g.kbase + koff + 64 * i);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R.v[r] = load_vec<vchunk_t>(g.vbase + voff + r * stok);
+    }
+  }
+
+  // Fold the step starting at `base` into (o, m_run, l_run).
+  __device__ __forceinline__ void compute(int base, int t_end, Regs &R, const qk_t (&q)[NQK]) {
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) sacc = MfK::run(__builtin_bit_cast(qk_t, R.k[i]), q[i], sacc);
+    // Masking is needed only on a partial step or an unreadable block.
+    const bool full = __all(base + STEP <= t_end && R.ok);
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = full || (R.ok && base + 4 * j + r < t_end);
+      x[r] = ok ? sacc[r] * scale_log2 : kNegInf;
+    }
+    if (!full) {
+      const vchunk_t z = {};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (x[r] == kNegInf) R.v[r] = z;  // keep NaN/Inf of unused slots out of P.V
+    }
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float msub = (m_new == kNegInf) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - msub);
+    float pf[4], lo[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(x[r] - msub);
+    l_run = l_run * alpha + ((pf[0] + pf[1]) + (pf[2] + pf[3]));
+    m_run = m_new;
+
+    // Rescale the accumulator rows g' = 4j + r by alpha of row g'.
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float a = shfl(alpha, 4 * j + r);
+#pragma unroll
+        for (int m = 0; m < CH; ++m) o[m][r] *= a;
+      }
+    }
+
+    const pv_t pa = pack4<T>(pf);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lo[r] = pf[r] - (float)pa[r];
+    const pv_t pl = pack4<T>(lo);
+#pragma unroll
+    for (int m = 0; m < CH; ++m) {
+      const uint32_t w0 = (m & 1) ? pair_hi(R.v[0][m >> 1], R.v[1][m >> 1])
+                                  : pair_lo(R.v[0][m >> 1], R.v[1][m >> 1]);
+      const uint32_t w1 = (m & 1) ? pair_hi(R.v[2][m >> 1], R.v[3][m >> 1])
+                                  : pair_lo(R.v[2][m >> 1], R.v[3][m >> 1]);
+      const u32x2 w = {w0, w1};
+      const pv_t vb = __builtin_bit_cast(pv_t, w);
+      o[m] = MfV::run(pa, vb, o[m]);
+      o[m] = MfV::run(pl, vb, o[m]);
+    }
+  }
+
+  // Sum the row sums over the four lane groups that hold each row.
+  __device__ __forceinline__ void reduce_rowsum() {
+    l_run += shfl_xor(l_run, 16);
+    l_run += shfl_xor(l_run, 32);
+  }
+
+  // After reduce_rowsum(): write this wave's normalised partial of rows
+  // g < ng as rows (slot0 + g) of the workspace: context, row max (natural
+  // log domain) and row sum.
+  __device__ __forceinline__ void store_partial(float *ws_o, float *ws_m, float *ws_l,
+                                                int64_t row0, int ng) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * j + r;
+      const float l = shfl(l_run, g);
+      const float mrow = shfl(m_run, g);
+      if (g >= ng) continue;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      float *dst = ws_o + (row0 + g) * D + n16 * CH;
+#pragma unroll
+      for (int m = 0; m < CH; m += 4) {
+        const f32x4 v = {o[m][r] * inv, o[m + 1][r] * inv, o[m + 2][r] * inv, o[m + 3][r] * inv};
+        store_vec<f32x4>(dst + m, v);
+      }
+      if (n16 == 0) {
+        ws_m[row0 + g] = l > 0.f ? mrow * kLn2 : kNegInf;
+        ws_l[row0 + g] = l;
+      }
+    }
+  }
+};
+
+}  // namespace clv

@@ -159,27 +159,48 @@ def decode_args(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                         max_context_len, scale)
 
 
+# Largest num_seqs * num_kv_heads * ceil(group / 16) of the balanced decode.
+BALANCED_MAX_SEGMENTS = 4096
+
+
+def balanced_supported(a: _native.DecodeArgs) -> bool:
+    group = a.num_heads // a.num_kv_heads
+    nseg = a.num_seqs * a.num_kv_heads * ((group + 15) // 16)
+    return (a.dtype in (_native.CLV_F16, _native.CLV_BF16) and a.head_dim in (64, 128)
+            and a.block_size >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
+
+
 def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_tables: torch.Tensor,
                     context_lens: torch.Tensor, block_size: int, max_context_len: int,
-                    scale: float | None = None, partition_size: int | None = None) -> None:
+                    scale: float | None = None, partition_size: int | None = None,
+                    num_waves: int = 0) -> None:
     """``out[s,h] = softmax(scale * q[s,h] . K^T) V`` over each sequence's paged context.
 
     Same arguments as the reference op (src/kernels/csrc/manager.cpp:19-27);
     ``scale`` defaults to 1/sqrt(head_dim) as in src/kernels/csrc/attention.cu:60.
     GQA follows from ``k_cache.shape[2] < q.shape[1]``. ``partition_size``:
-    None picks one, 0 forces a single pass, a positive multiple of 32 forces
-    split-K with that many tokens per partition.
+    None picks the schedule (the balanced stream decode where it applies,
+    with ``num_waves`` waves, 0 = the device default), 0 forces a single
+    pass per (sequence, kv head), a positive multiple of 32 forces split-K
+    with that many tokens per partition.
     """
     dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens)
     a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
                      max_context_len, scale)
     lib = _native.load()
+    stream = _stream(dev)
     if partition_size is None:
+        if balanced_supported(a):
+            nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
+                                                      a.head_dim, num_waves)
+            ws = splitk_workspace(dev, nbytes)
+            _native.check(lib.clv_paged_decode_balanced(a, num_waves, ws.data_ptr(), ws.numel(),
+                                                        stream), "clv_paged_decode_balanced")
+            return
         partition_size = choose_partition(a.num_seqs, a.num_kv_heads,
                                           a.num_heads // a.num_kv_heads, a.max_context_len,
                                           num_compute_units(dev))
-    stream = _stream(dev)
     if partition_size == 0 or a.max_context_len <= partition_size:
         _native.check(lib.clv_paged_decode(a, stream), "clv_paged_decode")
         return
@@ -201,6 +222,27 @@ def paged_decode_partials(a: _native.DecodeArgs, partition_size: int, workspace:
     _native.check(_native.load().clv_paged_decode_partials(
         a, partition_size, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
         stream), "clv_paged_decode_partials")
+
+
+def balanced_workspace_bytes(a: _native.DecodeArgs, num_waves: int = 0) -> int:
+    return _native.load().clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
+                                                       a.head_dim, num_waves)
+
+
+def balanced_partials(a: _native.DecodeArgs, num_waves: int, workspace: torch.Tensor,
+                      stream: int) -> None:
+    """First half of the balanced decode (stream kernel), see clv_balanced_partials."""
+    _native.check(_native.load().clv_balanced_partials(
+        a, num_waves, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        stream), "clv_balanced_partials")
+
+
+def balanced_reduce(a: _native.DecodeArgs, num_waves: int, workspace: torch.Tensor,
+                    stream: int) -> None:
+    """Second half of the balanced decode (merge into ``out``), see clv_balanced_reduce."""
+    _native.check(_native.load().clv_balanced_reduce(
+        a, num_waves, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        stream), "clv_balanced_reduce")
 
 
 def splitk_reduce(a: _native.DecodeArgs, partition_size: int, workspace: torch.Tensor,

@@ -180,6 +180,38 @@ int clv_splitk_reduce(const clv_decode_args *args, int32_t partition_size,
                       clv_stream_t stream);
 
 /*
+ * Balanced decode for ragged batches (fp16/bf16, head_dim 64 or 128,
+ * num_seqs * num_kv_heads * ceil(group/16) <= 4096): num_waves waves split
+ * the batch's flattened 16-token steps evenly, crossing sequence borders;
+ * each writes one partial per (sequence, kv head) it touches and a second
+ * kernel merges them with the same log-sum-exp rule as the split-K reduce.
+ * Same result as clv_paged_decode. num_waves <= 0 picks the device default
+ * (clv_default_num_waves()). No counterpart kernel exists in the reference.
+ */
+int clv_paged_decode_balanced(const clv_decode_args *args, int32_t num_waves,
+                              void *workspace, size_t workspace_bytes,
+                              clv_stream_t stream);
+
+/*
+ * The two halves of clv_paged_decode_balanced (same arguments): the stream
+ * kernel writing partials and the merge into `out`.
+ */
+int clv_balanced_partials(const clv_decode_args *args, int32_t num_waves,
+                          void *workspace, size_t workspace_bytes,
+                          clv_stream_t stream);
+int clv_balanced_reduce(const clv_decode_args *args, int32_t num_waves,
+                        const void *workspace, size_t workspace_bytes,
+                        clv_stream_t stream);
+
+/* Workspace bytes of clv_paged_decode_balanced (num_waves <= 0: default). */
+size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim,
+                                    int32_t num_waves);
+
+/* Default wave count of the balanced decode on the current device. */
+int32_t clv_default_num_waves(void);
+
+/*
  * Chunked prefill over paged KV (MFMA for fp16/bf16). No counterpart in the
  * reference; defined as equal, row by row, to successive append-then-attend
  * decode steps of CpuAttentionBackend.decode_layer

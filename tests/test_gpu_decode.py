@@ -16,13 +16,13 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def run_decode(q, k, v, tables, ctx, scale, partition_size=None, width=None):
+def run_decode(q, k, v, tables, ctx, scale, partition_size=None, width=None, num_waves=0):
     qg = q.to(DEV)
     out = torch.empty_like(qg)
     bt = padded_tables(tables, width).to(DEV)
     cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
     kernels.paged_attention(out, qg, k.to(DEV), v.to(DEV), bt, cl, k.shape[1], max(ctx),
-                            scale=scale, partition_size=partition_size)
+                            scale=scale, partition_size=partition_size, num_waves=num_waves)
     torch.cuda.synchronize()
     return out.cpu()
 
@@ -38,7 +38,7 @@ def case(seed, ctx, hq, hkv, d, bs, dtype, scale=None, value_scale=1.0):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (28, 4, 128), (32, 8, 64), (16, 1, 128),
                                       (32, 1, 64), (6, 2, 256), (4, 4, 32)])
-@pytest.mark.parametrize("partition", [0, 32, 512])
+@pytest.mark.parametrize("partition", [None, 0, 32, 512])
 def test_decode_matches_oracle(dtype, hq, hkv, d, partition):
     ctx = [1, 17, 31, 32, 33, 100, 511, 513, 1000, 0]
     print(f"decode dtype={dtype} hq={hq} hkv={hkv} d={d} P={partition}", flush=True)
@@ -54,11 +54,37 @@ def test_decode_matches_oracle(dtype, hq, hkv, d, partition):
 def test_decode_block_sizes(bs, dtype):
     ctx = [5, 64, 129, 300]
     q, k, v, tables, scale = case(bs, ctx, 14, 2, 128, bs, dtype)
-    for partition in (0, 64):
+    for partition in (None, 0, 64):
         width = max(len(t) for t in tables) + 3  # extra -1 padding columns
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition, width=width)
         ref = oa.paged_decode(q, k, v, tables, ctx, scale)
         assert_attention_close(got, ref, what=f"bs{bs} {dtype} P{partition}")
+
+
+@pytest.mark.parametrize("num_waves", [1, 3, 7, 64, 1000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_balanced_decode_wave_counts(num_waves, dtype):
+    """The balanced decode splits the batch's steps over any number of waves;
+    spans cross sequence and kv-head borders and skip empty contexts."""
+    ctx = [0, 1, 16, 17, 300, 0, 1000, 33, 2050]
+    print(f"balanced waves={num_waves} dtype={dtype}", flush=True)
+    q, k, v, tables, scale = case(num_waves + 3, ctx, 28, 4, 128, 16, dtype)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=None, num_waves=num_waves)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    assert_attention_close(got, ref, what=f"balanced W={num_waves}")
+    assert torch.equal(got[0].float(), torch.zeros(28, 128))
+
+
+def test_balanced_decode_many_segments():
+    """4096 (sequence, kv head) segments: the largest count the balanced
+    decode holds; one more sequence falls back to the split-K schedule."""
+    for nseq in (1024, 1025):
+        ctx = [int(x) for x in torch.randint(0, 70, (nseq,),
+                                              generator=torch.Generator().manual_seed(nseq))]
+        q, k, v, tables, scale = case(nseq, ctx, 8, 4, 64, 16, torch.float16)
+        got = run_decode(q, k, v, tables, ctx, scale)
+        ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+        assert_attention_close(got, ref, what=f"{nseq} seqs")
 
 
 def test_decode_strided_query_and_output():
@@ -157,7 +183,7 @@ def test_config_llama7b_mha_fp16(nseq):
     ctx = [2048] * nseq
     q, k, v, tables, scale = case(1002, ctx, 32, 32, 128, 16, torch.float16, value_scale=0.5)
     ref = oa.paged_decode(q, k, v, tables, ctx, scale)
-    for partition in (0, 512):
+    for partition in (None, 0, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"llama7b P{partition}")
 
@@ -170,11 +196,14 @@ def test_config_qwen7b_gqa_bf16_ragged():
     for partition in (None, 0, 256, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"qwen7b P{partition}")
+    got = run_decode(q, k, v, tables, ctx, scale, num_waves=37)
+    assert_attention_close(got, ref, what="qwen7b balanced W=37")
 
 
 def test_config_long_context_splitk_fp16():
     ctx = [32768, 32768]
     q, k, v, tables, scale = case(1004, ctx, 32, 8, 128, 16, torch.float16)
     ref = oa.paged_decode(q, k, v, tables, ctx, scale)
-    got = run_decode(q, k, v, tables, ctx, scale, partition_size=512)
-    assert_attention_close(got, ref, what="long-context P512")
+    for partition in (512, None):
+        got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
+        assert_attention_close(got, ref, what=f"long-context P{partition}")

@@ -170,6 +170,8 @@ def bench_decode(args, cfg):
     a = kernels.decode_args(out, w["q"], w["k"], w["v"], w["table"], w["ctx_dev"], w["bs"],
                             max_ctx, scale=w["scale"])
     part = args.partition if args.partition is not None else cfg["partition"]
+    if part is not None and part < 0:  # explicit request for the automatic schedule
+        part = None
     if part is None:
         if kernels.balanced_supported(a):
             mode = "balanced"
@@ -400,7 +402,7 @@ def main() -> int:
     ap.add_argument("--config", default="qwen7b",
                     choices=sorted(DECODE_CONFIGS) + ["prefill", "copy"])
     ap.add_argument("--partition", type=int, default=None,
-                    help="split-K partition size (0 = single pass; default: automatic)")
+                    help="split-K partition size (0 = single pass, -1 or default: automatic)")
     ap.add_argument("--waves", type=int, default=0,
                     help="waves of the balanced decode (0 = device default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

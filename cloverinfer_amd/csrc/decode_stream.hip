@@ -5,7 +5,9 @@
 // fixed number of waves W split the flattened space of 16-token steps
 //   (sequence, kv head, query-head chunk, step)    -- one "segment" per
 // (sequence, kv head, chunk), N steps in total
-// evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders.
+// evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders
+// (W is capped at N, so no wave is idle and a segment's partials come from
+// consecutive waves).
 // Each wave keeps its loads one step ahead (also across a border) and, for
 // every segment it touches, writes one partial (normalised context, row max,
 // row sum) to the workspace; stream_reduce merges the partials of each
@@ -78,7 +80,9 @@ __global__ void __launch_bounds__(kThreads) paged_decode_stream(const DecodePara
     s_seg[i] = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;
   __syncthreads();
   const int64_t N = block_exclusive_scan(s_seg, nseg, s_tmp);
-  const int64_t W = p.num_waves;
+  // At most one wave per step, so that every wave owns at least one step and
+  // each segment's partials come from consecutive waves.
+  const int64_t W = min((int64_t)p.num_waves, N);
   if (N > 0) {
     for (int i = threadIdx.x; i < nseg; i += kThreads) {
       const int a = s_seg[i], b = s_seg[i + 1];
@@ -227,7 +231,7 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int g = gall % 16;
   const int a = p.seg_prefix[seg], b = p.seg_prefix[seg + 1];
   const int64_t N = p.seg_prefix[p.num_segments];
-  const int64_t W = p.num_waves;
+  const int64_t W = min((int64_t)p.num_waves, N);
   int n = 0;
   if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
   const int64_t row0 = (int64_t)p.slot_prefix[seg] * 16 + g;

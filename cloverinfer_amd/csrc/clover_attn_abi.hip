@@ -5,6 +5,7 @@
 // between calls; errors come back as status codes.
 #include <math.h>
 #include <stddef.h>
+#include <stdlib.h>
 
 #include "clover_attn.h"
 #include "clv_internal.h"
@@ -236,11 +237,13 @@ int clv_paged_decode_splitk(const clv_decode_args *a, int32_t partition_size, vo
 
 int32_t clv_default_num_waves(void) {
   int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 2048;
+  if (hipGetDevice(&dev) != hipSuccess) return 1024;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 2048;
-  // Two 4-wave workgroups per compute unit: the decode kernel's occupancy.
-  return cus * 8;
+    return 1024;
+  // One wave per SIMD (4 per compute unit), each keeping four steps of loads
+  // in flight: on MI355X this streams the paged cache faster than more waves
+  // with shallower pipelines.
+  return cus * 4;
 }
 
 size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
@@ -258,6 +261,17 @@ size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t
 }  // extern "C"
 
 namespace {
+
+// Ring depth of the balanced decode: steps of loads each wave keeps in
+// flight (2, 3, 4 or 6). CLV_STREAM_DEPTH overrides the default for tuning.
+int stream_depth_setting() {
+  const char *env = getenv("CLV_STREAM_DEPTH");
+  if (env) {
+    const int d = atoi(env);
+    if (d == 2 || d == 3 || d == 4 || d == 6) return d;
+  }
+  return 4;
+}
 
 // Validates a balanced-decode call and lays the workspace out in p.
 int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
@@ -277,6 +291,7 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   const size_t rows = ((size_t)num_waves + (size_t)nseg) * 16;
   char *ws = (char *)workspace;
   p->num_waves = num_waves;
+  p->stream_depth = stream_depth_setting();
   p->num_segments = (int32_t)nseg;
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);

@@ -160,6 +160,17 @@ __device__ __forceinline__ void store_vec(void *p, V v) {
   *reinterpret_cast<V *>(p) = v;
 }
 
+// A wave-uniform 32-bit read through the scalar unit (s_load_dword). The
+// compiler only emits scalar loads where it can prove no store in the kernel
+// may clobber the address; kernels that store inside their main loop use this
+// for read-only tables so that the read does not join the vector-memory queue
+// (whose in-order counter would then also wait for every K/V load in flight).
+__device__ __forceinline__ int32_t scalar_load_i32(const int32_t *ptr) {
+  int32_t v;
+  asm("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(ptr));
+  return v;
+}
+
 // Raw buffer loads: a wave-uniform base in a buffer resource (SGPRs) plus a
 // 32-bit per-lane byte offset, so the hot loops keep no 64-bit per-lane
 // addresses. The range check (num_records) is set out of the way; callers
@@ -171,14 +182,26 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base) {
                                            0x00020000);
 }
 
-template <typename V> __device__ __forceinline__ V buf_load(rsrc_t r, uint32_t off);
+// Cache policy of a buffer load: kCacheDefault, or kCacheStream for data read
+// exactly once (the non-temporal hint: on MI355X streaming a large buffer this
+// way reads HBM at close to 90% of peak, against under 80% with the default).
+constexpr int kCacheDefault = 0;
+constexpr int kCacheStream = 2;
 
-template <> __device__ __forceinline__ u32x4 buf_load<u32x4>(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+template <typename V, int AUX = kCacheDefault>
+__device__ __forceinline__ V buf_load(rsrc_t r, uint32_t off);
+
+template <> __device__ __forceinline__ u32x4 buf_load<u32x4, kCacheDefault>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCacheDefault));
 }
-
-template <> __device__ __forceinline__ u32x2 buf_load<u32x2>(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+template <> __device__ __forceinline__ u32x4 buf_load<u32x4, kCacheStream>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCacheStream));
+}
+template <> __device__ __forceinline__ u32x2 buf_load<u32x2, kCacheDefault>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCacheDefault));
+}
+template <> __device__ __forceinline__ u32x2 buf_load<u32x2, kCacheStream>(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCacheStream));
 }
 
 }  // namespace clv

@@ -64,7 +64,8 @@ __device__ __forceinline__ OutDesc<T> out_desc(const DecodeParams &p, int s, int
 // with the loads of its next step in flight while the current one is
 // computed (two register sets), and the waves' partials are merged in LDS.
 template <typename T, int D, int NW, bool UNI>
-__global__ void __launch_bounds__(NW * 64) paged_decode_mfma(const DecodeParams p) {
+__global__ void __launch_bounds__(NW * 64)
+paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
   typedef DecodeWave<T, D, UNI> W;
   __shared__ WaveSmem<NW, 16, D> sm;
 
@@ -87,7 +88,7 @@ __global__ void __launch_bounds__(NW * 64) paged_decode_mfma(const DecodeParams 
   w.init(p);
   typename W::qk_t qop[W::NQK];
   w.load_q(p, s, h0, ng, qop);
-  const SegGeom geo = seg_geom<T>(p, s, kvh, t_end);
+  const SegGeom geo = seg_geom<T>(p, s, kvh, t_end, tables);
 
   // The prefetch is unconditional (a branch around it makes the compiler wait
   // for every outstanding load): past the wave's last step it re-reads that
@@ -203,9 +204,11 @@ hipError_t launch_mfma_td(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid(p.partition_size > 0 ? (unsigned)p.max_parts : 1u,
                   (unsigned)(p.num_kv_heads * p.n_gchunks), (unsigned)p.num_seqs);
   if (p.block_shift >= 4)
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true>), grid, dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true>), grid, dim3(NW * 64), 0, stream, p,
+                       p.block_tables);
   else
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false>), grid, dim3(NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false>), grid, dim3(NW * 64), 0, stream, p,
+                       p.block_tables);
   return hipGetLastError();
 }
 

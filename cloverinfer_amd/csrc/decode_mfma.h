@@ -11,7 +11,11 @@
 // 16-bit value and its 16-bit rounding residual, so P.V keeps fp32-level
 // accuracy); its B operand for output column block m is element m of the
 // lane's 4 V row chunks, regrouped with v_perm. Loads go through buffer
-// resources: a wave-uniform base (SGPRs) plus 32-bit lane offsets.
+// resources (a wave-uniform base in SGPRs plus 32-bit lane offsets). V rows
+// are read whole by each instruction and once per kv head, so they use the
+// streaming cache policy; a K instruction reads half of each 128-byte line
+// (the next one reads the other half), so K keeps the default policy, which
+// lets the second half hit in cache.
 #pragma once
 
 #include "attn_common.h"
@@ -29,6 +33,15 @@ __device__ __forceinline__ int clamp_ctx(const DecodeParams &p, int s) {
   return max(0, min(ctx, cap));
 }
 
+// Same for a wave-uniform s, read through the scalar unit (for kernels that
+// store to global memory inside their main loop).
+__device__ __forceinline__ int clamp_ctx(const DecodeParams &p, const int32_t *__restrict__ lens,
+                                         int s) {
+  const int ctx = scalar_load_i32(lens + s);
+  const int cap = min(p.max_context_len, p.max_blocks_per_seq << p.block_shift);
+  return max(0, min(ctx, cap));
+}
+
 // Where one (sequence, kv head) lives: its block-table row and pool bases.
 struct SegGeom {
   const int32_t *bt;
@@ -38,9 +51,10 @@ struct SegGeom {
 };
 
 template <typename T>
-__device__ __forceinline__ SegGeom seg_geom(const DecodeParams &p, int s, int kvh, int t_end) {
+__device__ __forceinline__ SegGeom seg_geom(const DecodeParams &p, int s, int kvh, int t_end,
+                                           const int32_t *__restrict__ tables) {
   SegGeom g;
-  g.bt = p.block_tables + (int64_t)s * p.max_blocks_per_seq;
+  g.bt = tables + (int64_t)s * p.max_blocks_per_seq;
   g.kbase = (const char *)p.k_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
   g.vbase = (const char *)p.v_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
   g.t_end = t_end;
@@ -105,13 +119,16 @@ struct DecodeWave {
 
   // Q rows h0 .. h0+ng-1 of sequence s as the B operand of S^T = K Q^T:
   // lane holds Q[g = n16][d = 32i + 8j .. +8] (zero for g >= ng).
+  // Every lane loads (a row >= ng re-reads row ng - 1 and is zeroed), so the
+  // number of loads in flight never depends on the lane mask.
   __device__ __forceinline__ void load_q(const DecodeParams &p, int s, int h0, int ng,
                                          qk_t (&q)[NQK]) const {
-    const T *qrow = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)(h0 + n16) * p.q_stride_head;
+    const int row = min(n16, ng - 1);
+    const T *qrow = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)(h0 + row) * p.q_stride_head;
 #pragma unroll
     for (int i = 0; i < NQK; ++i) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (n16 < ng) w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
+      u32x4 w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
+      if (n16 >= ng) w = (u32x4){0u, 0u, 0u, 0u};
       q[i] = __builtin_bit_cast(qk_t, w);
     }
   }
@@ -121,16 +138,16 @@ struct DecodeWave {
   // readable row and are masked when the step is computed.
   __device__ __forceinline__ void issue(const SegGeom &g, int base, Regs &R) const {
     if constexpr (UNI) {
-      const int blk = g.bt[base >> bshift];
+      const int blk = scalar_load_i32(g.bt + (base >> bshift));
       const bool ok = (unsigned)blk < nblocks;
       const int64_t off = ok ? blk * sblk + (base & bmask) * stok : 0;
       R.ok = ok;
       const rsrc_t rk = make_rsrc(g.kbase + off);
       const rsrc_t rv = make_rsrc(g.vbase + off);
 #pragma unroll
-      for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4>(rk, k_lane + 64u * i);
+      for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4, kCacheDefault>(rk, k_lane + 64u * i);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t>(rv, v_lane[r]);
+      for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t, kCacheStream>(rv, v_lane[r]);
     } else {
       const int tk = base + n16;
       const int kb = tk < g.t_end ? g.bt[tk >> bshift] : 0;

@@ -8,9 +8,9 @@
 // evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders
 // (W is capped at N, so no wave is idle and a segment's partials come from
 // consecutive waves).
-// Each wave keeps its loads one step ahead (also across a border) and, for
-// every segment it touches, writes one partial (normalised context, row max,
-// row sum) to the workspace; stream_reduce merges the partials of each
+// Each wave keeps three steps of loads in flight and, for every segment it
+// touches, writes one partial (normalised context, row max, row sum) to the
+// workspace; stream_reduce merges the partials of each
 // (sequence, query head) with the log-sum-exp rule of the reference's
 // partial-softmax merge (src/core/resident_kv_store.py:2497-2509).
 //
@@ -66,8 +66,15 @@ __device__ int block_exclusive_scan(int *buf, int n, int *tmp) {
   return total;
 }
 
-template <typename T, int D, bool UNI>
-__global__ void __launch_bounds__(kThreads) paged_decode_stream(const DecodeParams p) {
+template <typename T, int D, bool UNI, int DEPTH>
+__global__ void __launch_bounds__(kThreads)
+paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
+                    const int32_t *__restrict__ lens, float *__restrict__ ws_o,
+                    float *__restrict__ ws_m, float *__restrict__ ws_l,
+                    int32_t *__restrict__ seg_prefix, int32_t *__restrict__ slot_prefix) {
+  // Every global pointer is a separate restrict argument: with stores to the
+  // workspace inside the main loop, that is what lets the compiler keep the
+  // wave-uniform block-table reads scalar loads.
   typedef DecodeWave<T, D, UNI> WV;
   typedef typename WV::qk_t qk_t;
   __shared__ int s_seg[kStreamMaxSegments + 1];
@@ -77,7 +84,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_stream(const DecodePara
   const int nseg = p.num_segments;
   const int per_seq = p.num_kv_heads * p.n_gchunks;
   for (int i = threadIdx.x; i < nseg; i += kThreads)
-    s_seg[i] = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;
+    s_seg[i] = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;  // per-lane index: vector read
   __syncthreads();
   const int64_t N = block_exclusive_scan(s_seg, nseg, s_tmp);
   // At most one wave per step, so that every wave owns at least one step and
@@ -95,8 +102,8 @@ __global__ void __launch_bounds__(kThreads) paged_decode_stream(const DecodePara
   block_exclusive_scan(s_slot, nseg, s_tmp);
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= nseg; i += kThreads) {
-      p.seg_prefix[i] = s_seg[i];
-      p.slot_prefix[i] = s_slot[i];
+      seg_prefix[i] = s_seg[i];
+      slot_prefix[i] = s_slot[i];
     }
   }
 
@@ -120,70 +127,50 @@ __global__ void __launch_bounds__(kThreads) paged_decode_stream(const DecodePara
   WV w;
   w.init(p);
 
-  // Per-segment state of the step being computed.
-  int cur_s, cur_ng, cur_ctx, cur_first, cur_end;
-  SegGeom cur_geo;
-  qk_t q_cur[WV::NQK];
-  auto open_seg = [&](int sg, int &s_, int &ng_, int &ctx_, int &first_, int &end_, SegGeom &geo_,
-                      qk_t (&q_)[WV::NQK]) {
-    s_ = sg / per_seq;
-    const int rem = sg - s_ * per_seq;
+  // The span is cut at segment borders into runs. Each run loads its Q rows,
+  // keeps DEPTH steps of loads in flight (a ring of register sets refilled
+  // right after each step is folded) and ends with one partial.
+  int x = st;
+  while (x < en) {
+    while (uni(s_seg[seg + 1]) <= x) ++seg;  // skip empty segments
+    const int first = uni(s_seg[seg]);
+    const int last = min(en, uni(s_seg[seg + 1])) - 1;
+    const int s_ = seg / per_seq;
+    const int rem = seg - s_ * per_seq;
     const int kvh = rem / p.n_gchunks;
     const int g0 = (rem - kvh * p.n_gchunks) * 16;
-    ng_ = min(16, p.group - g0);
-    ctx_ = clamp_ctx(p, s_);
-    first_ = uni(s_seg[sg]);
-    end_ = uni(s_seg[sg + 1]);
-    geo_ = seg_geom<T>(p, s_, kvh, ctx_);
-    w.load_q(p, s_, kvh * p.group + g0, ng_, q_);
-  };
-  open_seg(seg, cur_s, cur_ng, cur_ctx, cur_first, cur_end, cur_geo, q_cur);
+    const int ng = min(16, p.group - g0);
+    const int ctx = clamp_ctx(p, lens, s_);
+    const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
+    qk_t q[WV::NQK];
+    w.load_q(p, s_, kvh * p.group + g0, ng, q);
 
-  int x = st;
-  typename WV::Regs A, B;
-  w.issue(cur_geo, (x - cur_first) * WV::STEP, A);
-
-  // One step: prefetch step x+1 (maybe of the next segment) into `nxt`,
-  // fold step x from `cur`, close the segment when it ends here.
-  auto step = [&](typename WV::Regs &cur, typename WV::Regs &nxt) -> bool {
-    const int nx = x + 1;
-    const bool more = nx < en;
-    const bool newseg = more && nx >= cur_end;
-    int n_seg = seg, n_s = cur_s, n_ng = cur_ng, n_ctx = cur_ctx, n_first = cur_first,
-        n_end = cur_end;
-    SegGeom n_geo = cur_geo;
-    qk_t q_next[WV::NQK];
-    if (newseg) {
-      n_seg = seg + 1;
-      while (uni(s_seg[n_seg + 1]) <= nx) ++n_seg;  // skip empty segments
-      open_seg(n_seg, n_s, n_ng, n_ctx, n_first, n_end, n_geo, q_next);
-    }
-    // Past the span end, re-read step x (cache resident, never used).
-    w.issue(n_geo, ((more ? nx : x) - n_first) * WV::STEP, nxt);
-    w.compute((x - cur_first) * WV::STEP, cur_ctx, cur, q_cur);
-    if (!more || newseg) {
-      w.reduce_rowsum();
-      const int piece = wid - wave_of(cur_first, W, N);
-      const int64_t row0 = ((int64_t)uni(s_slot[seg]) + piece) * 16;
-      w.store_partial(p.ws_o, p.ws_m, p.ws_l, row0, cur_ng);
-      w.reset();
-      if (!more) return false;
-      seg = n_seg;
-      cur_s = n_s;
-      cur_ng = n_ng;
-      cur_ctx = n_ctx;
-      cur_first = n_first;
-      cur_end = n_end;
-      cur_geo = n_geo;
+    // Ring of DEPTH register sets; past the run's last step it re-reads that
+    // step (cache resident, never used).
+    typename WV::Regs R[DEPTH];
 #pragma unroll
-      for (int i = 0; i < WV::NQK; ++i) q_cur[i] = q_next[i];
+    for (int i = 0; i < DEPTH; ++i) w.issue(geo, (min(x + i, last) - first) * WV::STEP, R[i]);
+    int c = x;
+    bool done = false;
+    while (!done) {
+#pragma unroll
+      for (int i = 0; i < DEPTH; ++i) {
+        if (!done) {
+          w.compute((c - first) * WV::STEP, ctx, R[i], q);
+          if (++c > last)
+            done = true;
+          else
+            w.issue(geo, (min(c + DEPTH - 1, last) - first) * WV::STEP, R[i]);
+        }
+      }
     }
-    x = nx;
-    return true;
-  };
-  for (;;) {
-    if (!step(A, B)) break;
-    if (!step(B, A)) break;
+
+    w.reduce_rowsum();
+    const int piece = wid - wave_of(first, W, N);
+    const int64_t row0 = ((int64_t)uni(s_slot[seg]) + piece) * 16;
+    w.store_partial(ws_o, ws_m, ws_l, row0, ng);
+    w.reset();
+    x = last + 1;
   }
 }
 
@@ -239,14 +226,28 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   merge_partials<T, D>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16, n, dst);
 }
 
-template <typename T, int D>
-hipError_t launch_stream_td(const DecodeParams &p, hipStream_t stream) {
+template <typename T, int D, int DEPTH>
+hipError_t launch_stream_tdd(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((p.num_waves + kWaves - 1) / kWaves));
   if (p.block_shift >= 4)
-    hipLaunchKernelGGL((paged_decode_stream<T, D, true>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH>), grid, dim3(kThreads), 0, stream,
+                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix,
+                       p.slot_prefix);
   else
-    hipLaunchKernelGGL((paged_decode_stream<T, D, false>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((paged_decode_stream<T, D, false, DEPTH>), grid, dim3(kThreads), 0, stream,
+                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix,
+                       p.slot_prefix);
   return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_stream_td(const DecodeParams &p, hipStream_t stream) {
+  switch (p.stream_depth) {
+    case 2: return launch_stream_tdd<T, D, 2>(p, stream);
+    case 6: return launch_stream_tdd<T, D, 6>(p, stream);
+    case 3: return launch_stream_tdd<T, D, 3>(p, stream);
+    default: return launch_stream_tdd<T, D, 4>(p, stream);
+  }
 }
 
 template <typename T>

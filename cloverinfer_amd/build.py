@@ -53,6 +53,10 @@ def compile_flags() -> list[str]:
         "-mcode-object-version=5",
         # Packed fp32 VALU ops stay off: write plain fp32 and let scalar ops run.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: the kernels fit in 256 VGPRs, and the
+        # AGPR form made the register allocator copy accumulators between the
+        # two files on every loop iteration.
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", INCLUDE_DIR,
         "-I", CSRC_DIR,
         "-Wall",

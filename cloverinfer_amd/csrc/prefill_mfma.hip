@@ -3,37 +3,78 @@
 // Semantics as in prefill.hip: query row i of sequence s sees cached
 // positions p <= context_lens[s] - n_s + i.
 //
-// Work decomposition: one workgroup (4 waves) per (sequence, kv head,
-// query tile). A query tile holds 128 rows = bq tokens x G query heads of
-// the kv head (row r is token r / G, head r % G), so the K/V tile staged in
-// LDS serves every query head of the group. Each wave owns 32 rows (two
-// 16-row MFMA tiles). Per 64-token KV tile a wave runs
-//   S^T[t, r] = K[t, :] . Q[r, :]    4 token tiles x 2 row tiles x D/32 MFMAs
-//   O[r, d]  += P[r, t] V[t, d]      2 token halves x 2 row tiles x 2 x D/16 MFMAs
-// (v_mfma_f32_16x16x32_{bf16,f16}), with an fp32 online softmax between.
-// As in the decode kernel, each lane's P values are already its A operand
-// of the PV product, and V is regrouped from 16-byte row chunks with v_perm.
+// Work decomposition: one workgroup (8 waves, two per SIMD) per (sequence,
+// kv head, query tile). A query tile holds up to 256 rows = bq tokens x G
+// query heads of the kv head (row r is token r / G, head r % G), so every K/V
+// tile staged in LDS serves all query heads of the group. Each wave owns 32
+// rows (two 16-row MFMA tiles) and fits in 256 VGPRs, so two waves share a
+// SIMD and one's softmax overlaps the other's MFMAs. Per 64-token K/V tile a
+// wave runs
+//   S^T[t, r] = K[t, :] . Q[r, :]   4 token tiles x 2 row tiles x D/32 MFMAs
+//   O[r, d]  += P[r, t] V[t, d]     2 token halves x 2 row tiles x D/16 MFMAs
+// (v_mfma_f32_16x16x32), with an fp32 online softmax between. The C layout
+// of the first product (lane holds row n16, tokens 4j..4j+3 of each 16-token
+// tile) is the A layout of the second, so P never leaves registers; V's B
+// operand is regrouped from 16-byte LDS row chunks with v_perm (output column
+// d = n16 * D/16 + m of MFMA m).
+//
+// P.V runs in fp16 for both input types. P is in [0, 2^8] (see the lazy
+// rescale below), where fp16 keeps 11 significant bits. bf16 V is converted
+// to fp16 once, when a tile is staged into LDS; that is exact for every bf16
+// value of magnitude below 2^16 (fp16 subnormals lose at most 2^-25 in
+// absolute terms). If any tile of a workgroup holds a larger (or infinite)
+// bf16 value, the workgroup recomputes its rows with an exact pass that keeps
+// V in bf16 and splits P into a bf16 value and its bf16 rounding residual
+// (two MFMAs, fp32-level accuracy). The exact pass is a separate loop, so it
+// costs the fast loop no registers.
+//
+// Online softmax: scores stay raw (scale folded into the exponent with one
+// fma), the running row maximum is only raised when a tile's maximum exceeds
+// it by more than 8 (log2 units), so the accumulator is rarely rescaled and
+// P stays below 2^8. Tiles fully below every row's causal limit, with all
+// block-table entries valid, skip the per-element masks.
+//
 // K/V tiles are double-buffered in LDS: the global loads of tile k+1 are in
-// flight while tile k is computed. Workgroup ids are remapped so that all
-// query tiles of one (sequence, kv head) run on the same XCD and share its L2.
+// flight while tile k is computed; block-table entries are fetched one tile
+// earlier still. Workgroup ids are remapped so that all query tiles of one
+// (sequence, kv head) run on the same XCD and share its L2.
 #include "attn_common.h"
+
+#include <type_traits>
 
 namespace clv {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRows = 128;  // query rows per workgroup
-constexpr int kBK = 64;     // KV tokens per tile
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRT = 2;                  // 16-row MFMA tiles per wave
+constexpr int kRows = kWaves * kRT * 16; // query rows per workgroup
+constexpr int kBK = 64;                 // K/V tokens per tile
+constexpr float kRescaleLog2 = 8.f;     // lazy-rescale threshold (log2 units)
 
 template <int CH> struct VChunkP;
 template <> struct VChunkP<8> { typedef u32x4 type; };
 template <> struct VChunkP<4> { typedef u32x2 type; };
 
+// Two bf16 values (one 32-bit word) as two fp16 values; records the largest
+// magnitude seen in `amax`.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float &amax) {
+  const float a = __builtin_bit_cast(float, w << 16);
+  const float b = __builtin_bit_cast(float, w & 0xffff0000u);
+  amax = fmaxf(amax, fmaxf(fabsf(a), fabsf(b)));
+  const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
+  const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
+  return lo | (hi << 16);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads)
 chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
-  typedef Mfma16x16x32<T> Mf;
-  typedef typename Mf::op_t op_t;
+  typedef Mfma16x16x32<T> MfQK;
+  typedef Mfma16x16x32<_Float16> MfPV;
+  typedef typename MfQK::op_t qk_t;
+  typedef typename MfPV::op_t pv_t;
+  constexpr bool kBf16 = sizeof(T) == 2 && !__is_same(T, _Float16);
   constexpr int NQK = D / 32;             // QK k-steps
   constexpr int CH = D / 16;              // PV MFMAs per (half, row tile)
   constexpr int LROW = D + 8;             // padded LDS row (elements)
@@ -43,15 +84,17 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   typedef typename VChunkP<CH>::type vchunk_t;
 
   __shared__ __attribute__((aligned(16))) T sK[2][kBK * LROW];
-  __shared__ __attribute__((aligned(16))) T sV[2][kBK * LROW];
-  __shared__ uint32_t sValid[2][kBK / 4];  // one byte per token: 1 = readable
+  // V rows: fp16 in the fast pass, T in the exact pass.
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kBK * LROW];
+  __shared__ __attribute__((aligned(4))) uint8_t sValid[2][kBK];  // 1 = the token's block is readable
+  __shared__ int sOvf;  // set when a bf16 V value did not fit fp16
 
   // XCD-aware remap: consecutive ids go round-robin over the 8 XCDs; give
   // each XCD a contiguous range of logical work items.
   const int per_xcd = gridDim.x / 8;
   const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
   if (L >= total) return;
-  const int qt = L % n_qtiles;
+  const int qt = n_qtiles - 1 - L % n_qtiles;  // longest query tiles first
   const int rest = L / n_qtiles;
   const int kvh = rest % p.num_kv_heads;
   const int s = rest / p.num_kv_heads;
@@ -70,7 +113,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15;
   const int j = lane >> 4;
 
@@ -83,184 +126,282 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   kv.block_shift = p.block_shift;
   kv.num_blocks = (unsigned)p.num_blocks;
 
+  // A negative scale is applied as a sign flip of Q, so that the softmax
+  // below only ever multiplies by c >= 0.
+  const float c = fabsf(p.scale_log2);
+  const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
+
   // Q (B operand of S^T = K Q^T) for this lane's rows 32w + 16rt + n16.
-  op_t qop[2][NQK];
-  int lim[2];  // last visible position of the lane's softmax row
+  u32x4 qop[kRT][NQK];  // kept as raw words: bit-cast to the operand type at each MFMA
+  int lim[kRT];  // last visible position of the lane's softmax row (-1: no row)
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < kRT; ++rt) {
     const int r = 32 * wave + 16 * rt + n16;
     const int tok = q0 + r / G;
     const bool ok = r < bq * G && tok < n_new;
     lim[rt] = ok ? base_pos + tok : -1;
-    const T *qrow = (const T *)p.q + (int64_t)(qs + tok) * p.q_stride_token +
+    const T *qrow = (const T *)p.q + (int64_t)(qs + (ok ? tok : q0)) * p.q_stride_token +
                     (int64_t)(kvh * G + r % G) * p.q_stride_head;
 #pragma unroll
     for (int i = 0; i < NQK; ++i) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (ok) w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
-      qop[rt][i] = __builtin_bit_cast(op_t, w);
+      u32x4 w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
+      w ^= qflip;
+      if (!ok) w = (u32x4){0u, 0u, 0u, 0u};
+      qop[rt][i] = w;
     }
   }
+  // Smallest causal limit over the wave's real rows (rows are ordered by
+  // token): tiles ending at or below it need no causal mask.
+  const int wave_row0 = 32 * wave;
+  const int wave_lim = (wave_row0 < bq * G && q0 + wave_row0 / G < n_new)
+                           ? base_pos + q0 + wave_row0 / G : -1;
 
   // Tile loader: thread handles chunk (tid % CPR) of rows tid / CPR + RPP*i.
   const int lchunk = tid % CPR;
   const int lrow = tid / CPR;
   u32x4 kreg[PASSES], vreg[PASSES];
-  bool rvalid[PASSES];
+  bool rvalid[PASSES];  // the loaded rows are readable tokens
+  int rblk[PASSES];     // block of each row of the tile to load next (-1: none)
+  // Block-table entries are fetched one tile before their rows are loaded and
+  // only turned into addresses then: a use right after the fetch would wait
+  // for every vector load in flight (the counter is in order).
+  auto fetch_blocks = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+      const int t = tile * kBK + lrow + RPP * i;
+      rblk[i] = (tile < ntiles && t < kv_end) ? kv.bt[t >> kv.block_shift] : -1;
+    }
+  };
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int t = tile * kBK + lrow + RPP * i;
-      const int64_t off = t < kv_end ? kv.row_offset(t) : -1;
-      rvalid[i] = off >= 0;
+      const bool ok = (unsigned)rblk[i] < kv.num_blocks;
+      const int64_t off = ok ? rblk[i] * kv.sblk + (t & ((1 << kv.block_shift) - 1)) * kv.stok : 0;
       const u32x4 z = {0u, 0u, 0u, 0u};
-      kreg[i] = rvalid[i] ? load_vec<u32x4>(kv.kbase + off + lchunk * 16) : z;
-      vreg[i] = rvalid[i] ? load_vec<u32x4>(kv.vbase + off + lchunk * 16) : z;
+      rvalid[i] = ok;
+      kreg[i] = ok ? load_vec<u32x4>(kv.kbase + off + lchunk * 16) : z;
+      vreg[i] = ok ? load_vec<u32x4>(kv.vbase + off + lchunk * 16) : z;
     }
   };
-  auto store_tile = [&](int buf) {
+  // Stage the loaded rows into LDS buffer buf. The fast pass stores V as
+  // fp16 and flags values that do not fit; the exact pass stores V as is.
+  auto store_tile = [&](int buf, auto exact_c) {
+    constexpr bool EXACT = decltype(exact_c)::value;
+    float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int row = lrow + RPP * i;
       store_vec<u32x4>(&sK[buf][row * LROW + lchunk * 8], kreg[i]);
-      store_vec<u32x4>(&sV[buf][row * LROW + lchunk * 8], vreg[i]);
-      if (lchunk == 0) ((uint8_t *)sValid[buf])[row] = rvalid[i] ? 1 : 0;
+      u32x4 v = vreg[i];
+      if constexpr (kBf16 && !EXACT) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e], amax);
+      }
+      store_vec<u32x4>(&sV[buf][row * LROW + lchunk * 8], v);
+      if (lchunk == 0) sValid[buf][row] = rvalid[i] ? 1 : 0;
     }
+    // 65504 is the largest finite fp16; bf16 has nothing between it and 2^16.
+    // NaN compares false here and converts to a NaN, as it should.
+    if (kBf16 && !EXACT && !(amax <= 65504.f)) sOvf = 1;
   };
 
-  f32x4 o[2][CH];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int m = 0; m < CH; ++m) o[rt][m] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {kNegInf, kNegInf};
-  float l_run[2] = {0.f, 0.f};
+  f32x4 o[kRT][CH];
+  float m_run[kRT], l_run[kRT];
 
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    const bool more = tile + 1 < ntiles;
-    if (more) load_tile(tile + 1);
-    const T *K = sK[buf];
-    const T *V = sV[buf];
-    const int t0 = tile * kBK;
-
-    // ---- scores: sacc[tt][rt][r] = S[row 16rt + n16][token t0 + 16tt + 4j + r]
-    f32x4 sacc[4][2];
+  // One pass over the K/V tiles. Returns whether a bf16 V value did not fit
+  // fp16 (fast pass only).
+  auto run_tiles = [&](auto exact_c) -> bool {
+    constexpr bool EXACT = decltype(exact_c)::value;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      sacc[tt][0] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      sacc[tt][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < kRT; ++rt) {
 #pragma unroll
-      for (int i = 0; i < NQK; ++i) {
-        const op_t a = __builtin_bit_cast(
-            op_t, load_vec<u32x4>(&K[(16 * tt + n16) * LROW + 32 * i + 8 * j]));
-        sacc[tt][0] = Mf::run(a, qop[0][i], sacc[tt][0]);
-        sacc[tt][1] = Mf::run(a, qop[1][i], sacc[tt][1]);
-      }
+      for (int m = 0; m < CH; ++m) o[rt][m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      m_run[rt] = kNegInf;
+      l_run[rt] = 0.f;
     }
-
-    // ---- online softmax per row tile
-    uint32_t vflags[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) vflags[tt] = sValid[buf][4 * tt + j];
-    float pf[2][16];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      float mx = kNegInf;
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int pos = t0 + 16 * tt + 4 * j + r;
-          const bool ok = ((vflags[tt] >> (8 * r)) & 0xffu) != 0 && pos <= lim[rt];
-          const float x = ok ? sacc[tt][rt][r] * p.scale_log2 : kNegInf;
-          pf[rt][4 * tt + r] = x;
-          mx = fmaxf(mx, x);
-        }
-      }
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[rt], mx);
-      const float msub = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[rt] - msub);
-      float psum = 0.f;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        pf[rt][k] = fast_exp2(pf[rt][k] - msub);
-        psum += pf[rt][k];
-      }
-      l_run[rt] = l_run[rt] * alpha + psum;
-      m_run[rt] = m_new;
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float a = shfl(alpha, 4 * j + r);
-#pragma unroll
-          for (int m = 0; m < CH; ++m) o[rt][m][r] *= a;
-        }
-      }
+    if (tid == 0) sOvf = 0;
+    fetch_blocks(0);
+    if (ntiles > 0) {
+      load_tile(0);
+      fetch_blocks(1);
+      __syncthreads();  // sOvf cleared (and the previous pass done with LDS)
+      store_tile(0, exact_c);
     }
+    __syncthreads();
 
-    // ---- O += P V, two 32-token halves
+    for (int tile = 0; tile < ntiles; ++tile) {
+      const int buf = tile & 1;
+      const bool more = tile + 1 < ntiles;
+      if (more) {
+        load_tile(tile + 1);     // block ids fetched last iteration
+        fetch_blocks(tile + 2);  // block-table entries for the tile after
+      }
+      const T *K = sK[buf];
+      const int t0 = tile * kBK;
+
+      // full: every token of the tile is readable and visible to every row of
+      // this wave, so no per-element mask is needed.
+      const bool all_valid = __all(sValid[buf][lane] != 0);
+      const bool full = all_valid && t0 + kBK - 1 <= wave_lim;
+
+      // The tile is processed in two 32-token halves: scores, softmax, P.V.
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      vchunk_t vr[8];
+      for (int half = 0; half < 2; ++half) {
+        // ---- scores: sacc[h][rt][e] = S'[row 16rt + n16][token t0 + 32half + 16h + 4j + e]
+        f32x4 sacc[2][kRT];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vr[4 * h + r] = load_vec<vchunk_t>(&V[(32 * half + 16 * h + 4 * j + r) * LROW + n16 * CH]);
-      // P split into its 16-bit value and the 16-bit rounding residual, so
-      // that P.V keeps fp32-level accuracy.
-      op_t pa[2], pl[2];
+          for (int rt = 0; rt < kRT; ++rt) sacc[h][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        float x[8], lo[8];
+          for (int i = 0; i < NQK; ++i) {
+            const qk_t a = __builtin_bit_cast(
+                qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * LROW + 32 * i + 8 * j]));
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt)
+              sacc[h][rt] = MfQK::run(a, __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
+          }
+        }
+
+        // ---- online softmax
+        float pf[kRT][8];
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          float mx = kNegInf;
+          if (full) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sacc[h][rt][e]);
+          } else {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint32_t vf =
+                  *reinterpret_cast<const uint32_t *>(&sValid[buf][32 * half + 16 * h + 4 * j]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int pos = t0 + 32 * half + 16 * h + 4 * j + e;
+                const bool ok = ((vf >> (8 * e)) & 0xffu) != 0 && pos <= lim[rt];
+                if (!ok) sacc[h][rt][e] = kNegInf;
+                mx = fmaxf(mx, sacc[h][rt][e]);
+              }
+            }
+          }
+          mx = fmaxf(mx, shfl_xor(mx, 16));
+          mx = fmaxf(mx, shfl_xor(mx, 32));
+          // Raise the running max only when the scores exceed it by > 2^8 (or
+          // it is still -inf); c == 0 never rescales (every p is 1).
+          const bool grow = (mx - m_run[rt]) * c > kRescaleLog2;
+          if (__any(grow)) {
+            const float m_new = fmaxf(m_run[rt], mx);
+            // 0 when the row had no visible token yet, 1 if its max is unchanged.
+            const float alpha = m_new == kNegInf ? 1.f : fast_exp2((m_run[rt] - m_new) * c);
+            m_run[rt] = m_new;
+            l_run[rt] *= alpha;
+            // Row 4j + e of o[rt][m] is element e.
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float a = shfl(alpha, 4 * j + e);
+#pragma unroll
+              for (int m = 0; m < CH; ++m) o[rt][m][e] *= a;
+            }
+          }
+          const float msub = m_run[rt] == kNegInf ? 0.f : m_run[rt] * c;
+          float psum = 0.f;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = sacc[h][rt][e];
+              float pr = fast_exp2(__builtin_fmaf(x, c, -msub));
+              if (!full) pr = x == kNegInf ? 0.f : pr;
+              pf[rt][4 * h + e] = pr;
+              psum += pr;
+            }
+          }
+          l_run[rt] += psum;
+        }
+
+        // ---- O += P V over the half's 32 tokens. P's k-slot 4h + e and V's
+        // row chunk vr[4h + e] are both token 32half + 16h + 4j + e; MFMA m
+        // produces output columns d = n16 * CH + m.
+        vchunk_t vr[8];
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) x[4 * h + r] = pf[rt][4 * (2 * half + h) + r];
-        pa[rt] = pack8<T>(x);
+          for (int e = 0; e < 4; ++e)
+            vr[4 * h + e] = load_vec<vchunk_t>(
+                &sV[buf][(32 * half + 16 * h + 4 * j + e) * LROW + n16 * CH]);
+        if constexpr (!EXACT) {
+          pv_t pa[kRT];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) lo[k] = x[k] - (float)pa[rt][k];
-        pl[rt] = pack8<T>(lo);
-      }
+          for (int rt = 0; rt < kRT; ++rt) pa[rt] = pack8<_Float16>(pf[rt]);
 #pragma unroll
-      for (int m = 0; m < CH; ++m) {
-        u32x4 w;
+          for (int m = 0; m < CH; ++m) {
+            u32x4 w;
 #pragma unroll
-        for (int q2 = 0; q2 < 4; ++q2) {
-          const uint32_t a = vr[2 * q2][m >> 1];
-          const uint32_t b = vr[2 * q2 + 1][m >> 1];
-          w[q2] = (m & 1) ? pair_hi(a, b) : pair_lo(a, b);
+            for (int q2 = 0; q2 < 4; ++q2) {
+              const uint32_t a = vr[2 * q2][m >> 1];
+              const uint32_t b = vr[2 * q2 + 1][m >> 1];
+              w[q2] = (m & 1) ? pair_hi(a, b) : pair_lo(a, b);
+            }
+            const pv_t vb = __builtin_bit_cast(pv_t, w);
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt) o[rt][m] = MfPV::run(pa[rt], vb, o[rt][m]);
+          }
+        } else {
+          // bf16 V, P split into its bf16 value and bf16 residual.
+          typedef Mfma16x16x32<__bf16> MfB;
+          typedef typename MfB::op_t b_t;
+          b_t pa[kRT], pl[kRT];
+#pragma unroll
+          for (int rt = 0; rt < kRT; ++rt) {
+            float lo[8];
+            pa[rt] = pack8<__bf16>(pf[rt]);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) lo[k] = pf[rt][k] - (float)pa[rt][k];
+            pl[rt] = pack8<__bf16>(lo);
+          }
+#pragma unroll
+          for (int m = 0; m < CH; ++m) {
+            u32x4 w;
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+              const uint32_t a = vr[2 * q2][m >> 1];
+              const uint32_t b = vr[2 * q2 + 1][m >> 1];
+              w[q2] = (m & 1) ? pair_hi(a, b) : pair_lo(a, b);
+            }
+            const b_t vb = __builtin_bit_cast(b_t, w);
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt) {
+              o[rt][m] = MfB::run(pa[rt], vb, o[rt][m]);
+              o[rt][m] = MfB::run(pl[rt], vb, o[rt][m]);
+            }
+          }
         }
-        const op_t vb = __builtin_bit_cast(op_t, w);
-        o[0][m] = Mf::run(pa[0], vb, o[0][m]);
-        o[1][m] = Mf::run(pa[1], vb, o[1][m]);
-        o[0][m] = Mf::run(pl[0], vb, o[0][m]);
-        o[1][m] = Mf::run(pl[1], vb, o[1][m]);
       }
-    }
 
-    if (more) store_tile(buf ^ 1);
-    __syncthreads();
+      if (more) store_tile(buf ^ 1, exact_c);
+      __syncthreads();
+    }
+    return kBf16 && !EXACT && sOvf != 0;
+  };
+
+  const bool overflow = run_tiles(std::false_type{});
+  if constexpr (kBf16) {
+    if (overflow) run_tiles(std::true_type{});
   }
 
-  // ---- normalise and store rows 32w + 16rt + 4j + r
+  // ---- normalise and store rows 32w + 16rt + 4j + e
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < kRT; ++rt) {
     l_run[rt] += shfl_xor(l_run[rt], 16);
     l_run[rt] += shfl_xor(l_run[rt], 32);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float l = shfl(l_run[rt], 4 * j + r);
-      const int row = 32 * wave + 16 * rt + 4 * j + r;
+    for (int e = 0; e < 4; ++e) {
+      const float l = shfl(l_run[rt], 4 * j + e);
+      const int row = 32 * wave + 16 * rt + 4 * j + e;
       const int tok = q0 + row / G;
       if (row >= bq * G || tok >= n_new) continue;
       const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -269,8 +410,8 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       uint32_t u[CH / 2];
 #pragma unroll
       for (int m = 0; m < CH; m += 2) {
-        const uint32_t lo = __builtin_bit_cast(uint16_t, (T)(o[rt][m][r] * inv));
-        const uint32_t hi = __builtin_bit_cast(uint16_t, (T)(o[rt][m + 1][r] * inv));
+        const uint32_t lo = __builtin_bit_cast(uint16_t, (T)(o[rt][m][e] * inv));
+        const uint32_t hi = __builtin_bit_cast(uint16_t, (T)(o[rt][m + 1][e] * inv));
         u[m / 2] = lo | (hi << 16);
       }
       if constexpr (CH == 8) {

@@ -88,3 +88,42 @@ def test_prefill_rows_equal_decode_steps_full_config():
                             max(rows_ctx), scale=scale, partition_size=0)
     torch.cuda.synchronize()
     assert_attention_close(got, out.cpu(), what="prefill rows vs decode")
+
+
+@pytest.mark.parametrize("bs", [4, 8, 32, 64])
+def test_prefill_block_sizes(bs):
+    cached, new = [0, 33, 200], [70, 5, 64]
+    q, k, v, tables, ctx, qsl = build(300 + bs, cached, new, 16, 4, 128, bs, torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what=f"prefill bs{bs}")
+
+
+@pytest.mark.parametrize("scale", [-0.125, 0.0, 0.02])
+def test_prefill_scales(scale):
+    """Negative scales (applied as a sign flip of q), zero (uniform weights)
+    and a small positive scale."""
+    cached, new = [90, 0], [40, 130]
+    q, k, v, tables, ctx, qsl = build(41, cached, new, 8, 2, 64, 16, torch.float16)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what=f"prefill scale {scale}")
+
+
+def test_prefill_bf16_values_beyond_fp16_range():
+    """bf16 V values of magnitude >= 2^16 do not fit the fp16 P.V path: the
+    workgroups that see them take the exact bf16 pass. Large scores too, so
+    that the running maximum is raised several times."""
+    cached, new = [300, 1000], [200, 300]
+    q, k, v, tables, ctx, qsl = build(57, cached, new, 32, 8, 128, 16, torch.bfloat16)
+    # A few huge V values in the context of sequence 1 only (sequence 0 keeps
+    # the fast pass), plus a scaled-up stretch of keys.
+    blk = tables[1][3]
+    v[blk, 2, 5, :] = 3.0e5
+    v[blk, 7, 0, 17] = -1.0e30
+    k[tables[1][10], :, :, :] *= 6
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what="prefill bf16 beyond fp16 range")

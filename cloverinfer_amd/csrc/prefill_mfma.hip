@@ -15,8 +15,8 @@
 // (v_mfma_f32_16x16x32), with an fp32 online softmax between. The C layout
 // of the first product (lane holds row n16, tokens 4j..4j+3 of each 16-token
 // tile) is the A layout of the second, so P never leaves registers; V's B
-// operand is regrouped from 16-byte LDS row chunks with v_perm (output column
-// d = n16 * D/16 + m of MFMA m).
+// operand comes straight from LDS with transposing reads (ds_read_b64_tr_b16),
+// so MFMA m produces output columns d = 16m + n16.
 //
 // P.V runs in fp16 for both input types. P is in [0, 2^8] (see the lazy
 // rescale below), where fp16 keeps 11 significant bits. bf16 V is converted
@@ -52,9 +52,19 @@ constexpr int kRows = kWaves * kRT * 16; // query rows per workgroup
 constexpr int kBK = 64;                 // K/V tokens per tile
 constexpr float kRescaleLog2 = 8.f;     // lazy-rescale threshold (log2 units)
 
-template <int CH> struct VChunkP;
-template <> struct VChunkP<8> { typedef u32x4 type; };
-template <> struct VChunkP<4> { typedef u32x2 type; };
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8 bytes read by lane 4k + i / 4 as its element k (k = 0..3)
+// (measured on gfx950). So when lanes 4k..4k+3 of a group read columns
+// c0 + 4(i % 4) .. +3 of one row t_k, lane i gets column c0 + i of rows
+// t_0..t_3: four K-consecutive elements of an MFMA B operand. Two such reads
+// (rows of k-slots 0..3 and 4..7) make the lane's 8-element operand.
+__device__ __forceinline__ u32x4 vt_read(const uint16_t *lo, const uint16_t *hi) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)lo);
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)hi);
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return (u32x4){ua[0], ua[1], ub[0], ub[1]};
+}
 
 // Two bf16 values (one 32-bit word) as two fp16 values; records the largest
 // magnitude seen in `amax`.
@@ -77,15 +87,19 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   constexpr bool kBf16 = sizeof(T) == 2 && !__is_same(T, _Float16);
   constexpr int NQK = D / 32;             // QK k-steps
   constexpr int CH = D / 16;              // PV MFMAs per (half, row tile)
-  constexpr int LROW = D + 8;             // padded LDS row (elements)
+  // LDS row strides (elements), measured on gfx950: the K reads
+  // (ds_read_b128, lane row = lane % 16) are conflict-free at a stride of
+  // 32 mod 64 bytes; the transposed V reads (four rows per 16-lane group)
+  // need a stride that is not a multiple of 64 bytes.
+  constexpr int KROW = D + 16;
+  constexpr int VROW = D + 16;
   constexpr int CPR = D * 2 / 16;         // 16-byte chunks per row
   constexpr int RPP = kThreads / CPR;     // rows per load pass
   constexpr int PASSES = kBK / RPP;       // load passes per tile
-  typedef typename VChunkP<CH>::type vchunk_t;
 
-  __shared__ __attribute__((aligned(16))) T sK[2][kBK * LROW];
+  __shared__ __attribute__((aligned(16))) T sK[2][kBK * KROW];
   // V rows: fp16 in the fast pass, T in the exact pass.
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kBK * LROW];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kBK * VROW];
   __shared__ __attribute__((aligned(4))) uint8_t sValid[2][kBK];  // 1 = the token's block is readable
   __shared__ int sOvf;  // set when a bf16 V value did not fit fp16
 
@@ -192,13 +206,13 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int row = lrow + RPP * i;
-      store_vec<u32x4>(&sK[buf][row * LROW + lchunk * 8], kreg[i]);
+      store_vec<u32x4>(&sK[buf][row * KROW + lchunk * 8], kreg[i]);
       u32x4 v = vreg[i];
       if constexpr (kBf16 && !EXACT) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e], amax);
       }
-      store_vec<u32x4>(&sV[buf][row * LROW + lchunk * 8], v);
+      store_vec<u32x4>(&sV[buf][row * VROW + lchunk * 8], v);
       if (lchunk == 0) sValid[buf][row] = rvalid[i] ? 1 : 0;
     }
     // 65504 is the largest finite fp16; bf16 has nothing between it and 2^16.
@@ -257,7 +271,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
 #pragma unroll
           for (int i = 0; i < NQK; ++i) {
             const qk_t a = __builtin_bit_cast(
-                qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * LROW + 32 * i + 8 * j]));
+                qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * KROW + 32 * i + 8 * j]));
 #pragma unroll
             for (int rt = 0; rt < kRT; ++rt)
               sacc[h][rt] = MfQK::run(a, __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
@@ -326,27 +340,17 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
         // ---- O += P V over the half's 32 tokens. P's k-slot 4h + e and V's
         // row chunk vr[4h + e] are both token 32half + 16h + 4j + e; MFMA m
         // produces output columns d = n16 * CH + m.
-        vchunk_t vr[8];
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            vr[4 * h + e] = load_vec<vchunk_t>(
-                &sV[buf][(32 * half + 16 * h + 4 * j + e) * LROW + n16 * CH]);
+        // B operand of MFMA m (output columns d = 16m + n16): lane (n16, j)
+        // needs V[token of k-slot 4h + kk][16m + n16], two transposed LDS
+        // reads (h = 0, 1) of four tokens each (see vt_read).
+        const uint16_t *vrow = &sV[buf][(32 * half + 4 * j + (n16 >> 2)) * VROW + 4 * (n16 & 3)];
         if constexpr (!EXACT) {
           pv_t pa[kRT];
 #pragma unroll
           for (int rt = 0; rt < kRT; ++rt) pa[rt] = pack8<_Float16>(pf[rt]);
 #pragma unroll
           for (int m = 0; m < CH; ++m) {
-            u32x4 w;
-#pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-              const uint32_t a = vr[2 * q2][m >> 1];
-              const uint32_t b = vr[2 * q2 + 1][m >> 1];
-              w[q2] = (m & 1) ? pair_hi(a, b) : pair_lo(a, b);
-            }
-            const pv_t vb = __builtin_bit_cast(pv_t, w);
+            const pv_t vb = __builtin_bit_cast(pv_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
 #pragma unroll
             for (int rt = 0; rt < kRT; ++rt) o[rt][m] = MfPV::run(pa[rt], vb, o[rt][m]);
           }
@@ -365,14 +369,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
           }
 #pragma unroll
           for (int m = 0; m < CH; ++m) {
-            u32x4 w;
-#pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-              const uint32_t a = vr[2 * q2][m >> 1];
-              const uint32_t b = vr[2 * q2 + 1][m >> 1];
-              w[q2] = (m & 1) ? pair_hi(a, b) : pair_lo(a, b);
-            }
-            const b_t vb = __builtin_bit_cast(b_t, w);
+            const b_t vb = __builtin_bit_cast(b_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
 #pragma unroll
             for (int rt = 0; rt < kRT; ++rt) {
               o[rt][m] = MfB::run(pa[rt], vb, o[rt][m]);
@@ -405,22 +402,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       const int tok = q0 + row / G;
       if (row >= bq * G || tok >= n_new) continue;
       const float inv = l > 0.f ? 1.f / l : 0.f;
+      // Lane n16 of MFMA m holds column d = 16m + n16.
       T *dst = (T *)p.out + (int64_t)(qs + tok) * p.out_stride_token +
-               (int64_t)(kvh * G + row % G) * p.out_stride_head + n16 * CH;
-      uint32_t u[CH / 2];
+               (int64_t)(kvh * G + row % G) * p.out_stride_head + n16;
 #pragma unroll
-      for (int m = 0; m < CH; m += 2) {
-        const uint32_t lo = __builtin_bit_cast(uint16_t, (T)(o[rt][m][e] * inv));
-        const uint32_t hi = __builtin_bit_cast(uint16_t, (T)(o[rt][m + 1][e] * inv));
-        u[m / 2] = lo | (hi << 16);
-      }
-      if constexpr (CH == 8) {
-        const u32x4 w = {u[0], u[1], u[2], u[3]};
-        store_vec<u32x4>(dst, w);
-      } else {
-        const u32x2 w = {u[0], u[1]};
-        store_vec<u32x2>(dst, w);
-      }
+      for (int m = 0; m < CH; ++m) dst[16 * m] = (T)(o[rt][m][e] * inv);
     }
   }
 }

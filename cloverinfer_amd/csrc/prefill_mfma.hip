@@ -34,8 +34,9 @@
 // P stays below 2^8. Tiles fully below every row's causal limit, with all
 // block-table entries valid, skip the per-element masks.
 //
-// K/V tiles are double-buffered in LDS: the global loads of tile k+1 are in
-// flight while tile k is computed; block-table entries are fetched one tile
+// K/V tiles go through a three-stage LDS ring: the global loads of tile k+1
+// are in flight while tile k is computed, and the P.V of the last half-step
+// of tile k - 1 still reads its V; block-table entries are fetched one tile
 // earlier still. Workgroup ids are remapped so that all query tiles of one
 // (sequence, kv head) run on the same XCD and share its L2.
 #include "attn_common.h"
@@ -97,10 +98,10 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   constexpr int RPP = kThreads / CPR;     // rows per load pass
   constexpr int PASSES = kBK / RPP;       // load passes per tile
 
-  __shared__ __attribute__((aligned(16))) T sK[2][kBK * KROW];
+  __shared__ __attribute__((aligned(16))) T sK[3][kBK * KROW];
   // V rows: fp16 in the fast pass, T in the exact pass.
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kBK * VROW];
-  __shared__ __attribute__((aligned(4))) uint8_t sValid[2][kBK];  // 1 = the token's block is readable
+  __shared__ __attribute__((aligned(16))) uint16_t sV[3][kBK * VROW];
+  __shared__ __attribute__((aligned(4))) uint8_t sValid[3][kBK];  // 1 = the token's block is readable
   __shared__ int sOvf;  // set when a bf16 V value did not fit fp16
 
   // XCD-aware remap: consecutive ids go round-robin over the 8 XCDs; give
@@ -141,8 +142,10 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   kv.num_blocks = (unsigned)p.num_blocks;
 
   // A negative scale is applied as a sign flip of Q, so that the softmax
-  // below only ever multiplies by c >= 0.
-  const float c = fabsf(p.scale_log2);
+  // below only ever multiplies by c > 0. A zero scale becomes 2^-126: every
+  // weight is then 1 to far below fp32 resolution, and masked scores (-inf)
+  // still weigh exactly 0.
+  const float c = fmaxf(fabsf(p.scale_log2), 0x1p-126f);
   const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
 
   // Q (B operand of S^T = K Q^T) for this lane's rows 32w + 16rt + n16.
@@ -221,19 +224,162 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   };
 
   f32x4 o[kRT][CH];
-  float m_run[kRT], l_run[kRT];
+  float m_run[kRT];
+  // Row sums of P, accumulated by MFMA against an all-ones B operand (so in
+  // the C layout of o: element e is row 4j + e), consistent with the
+  // rounded P that P.V uses.
+  f32x4 lsum[kRT];
 
-  // One pass over the K/V tiles. Returns whether a bf16 V value did not fit
-  // fp16 (fast pass only).
+  // One pass over the K/V tiles, software-pipelined per 32-token half-step
+  // g (tile g / 2, half g % 2):
+  //   M(g): scores of g (QK MFMAs), then P.V of g - 1 (PV MFMAs)
+  //   V(g): online softmax of g (VALU), producing the P operand of g.
+  // Waves 0-3 run M V M V per tile, waves 4-7 (the other wave of each
+  // SIMD) run V M V M with their softmax one step behind, so that on every
+  // SIMD one wave's softmax overlaps the other's MFMAs. P.V of g - 1 may read
+  // the previous tile, hence three LDS stages. Returns whether a bf16 V value
+  // did not fit fp16 (fast pass only).
   auto run_tiles = [&](auto exact_c) -> bool {
     constexpr bool EXACT = decltype(exact_c)::value;
+    typedef Mfma16x16x32<__bf16> MfB;
+    typedef typename std::conditional<EXACT, typename MfB::op_t, pv_t>::type p_t;
 #pragma unroll
     for (int rt = 0; rt < kRT; ++rt) {
 #pragma unroll
       for (int m = 0; m < CH; ++m) o[rt][m] = (f32x4){0.f, 0.f, 0.f, 0.f};
       m_run[rt] = kNegInf;
-      l_run[rt] = 0.f;
+      lsum[rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
+    f32x4 sacc[2][kRT];     // scores of the step between M and V
+    p_t pa[kRT], pl[kRT];   // P of the step between V and the next M (pl: exact pass)
+
+    // Scores of step g: sacc[h][rt][e] = S'[row 16rt + n16][token 32(g%2) + 16h + 4j + e].
+    auto qk = [&](int g) {
+      const T *K = sK[(g >> 1) % 3];
+      const int half = g & 1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) sacc[h][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < NQK; ++i) {
+          const qk_t a = __builtin_bit_cast(
+              qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * KROW + 32 * i + 8 * j]));
+#pragma unroll
+          for (int rt = 0; rt < kRT; ++rt)
+            sacc[h][rt] = MfQK::run(a, __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
+        }
+      }
+    };
+    // O += P V for step g. B operand of MFMA m (output columns 16m + n16):
+    // lane (n16, j) needs V[token of k-slot 4h + kk][16m + n16], two
+    // transposed LDS reads (h = 0, 1) of four tokens each (see vt_read).
+    const p_t ones = __builtin_bit_cast(
+        p_t, (u32x4){EXACT ? 0x3f803f80u : 0x3c003c00u, EXACT ? 0x3f803f80u : 0x3c003c00u,
+                     EXACT ? 0x3f803f80u : 0x3c003c00u, EXACT ? 0x3f803f80u : 0x3c003c00u});
+    auto pv = [&](int g) {
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        if constexpr (!EXACT) {
+          lsum[rt] = MfPV::run(pa[rt], ones, lsum[rt]);
+        } else {
+          lsum[rt] = MfB::run(pa[rt], ones, lsum[rt]);
+          lsum[rt] = MfB::run(pl[rt], ones, lsum[rt]);
+        }
+      }
+      const uint16_t *vrow = &sV[(g >> 1) % 3][(32 * (g & 1) + 4 * j + (n16 >> 2)) * VROW +
+                                               4 * (n16 & 3)];
+#pragma unroll
+      for (int m = 0; m < CH; ++m) {
+        const p_t vb =
+            __builtin_bit_cast(p_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+          if constexpr (!EXACT) {
+            o[rt][m] = MfPV::run(pa[rt], vb, o[rt][m]);
+          } else {
+            o[rt][m] = MfB::run(pa[rt], vb, o[rt][m]);
+            o[rt][m] = MfB::run(pl[rt], vb, o[rt][m]);
+          }
+        }
+      }
+    };
+    // Scores of step g that a row may not see (unreadable block, past the
+    // row's causal limit) become -inf: they drop out of the row max and, as
+    // c > 0, weigh exp2(-inf) = 0. Only steps of tiles that are not full.
+    auto mask_step = [&](int g) {
+      const int buf = (g >> 1) % 3;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t vf =
+            *reinterpret_cast<const uint32_t *>(&sValid[buf][32 * (g & 1) + 16 * h + 4 * j]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int pos = 32 * g + 16 * h + 4 * j + e;
+          const bool readable = ((vf >> (8 * e)) & 0xffu) != 0;
+#pragma unroll
+          for (int rt = 0; rt < kRT; ++rt)
+            if (!(readable && pos <= lim[rt])) sacc[h][rt][e] = kNegInf;
+        }
+      }
+    };
+    // Online softmax of step g.
+    auto softmax = [&](int g, bool full) {
+      if (!full) mask_step(g);
+      float pf[kRT][8];
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sacc[h][rt][e]);
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        // Raise the running max only when the scores exceed it by > 2^8 (or
+        // it is still -inf).
+        const bool grow = (mx - m_run[rt]) * c > kRescaleLog2;
+        if (__any(grow)) {
+          const float m_new = fmaxf(m_run[rt], mx);
+          // 0 when the row had no visible token yet, 1 if its max is unchanged.
+          const float alpha = m_new == kNegInf ? 1.f : fast_exp2((m_run[rt] - m_new) * c);
+          m_run[rt] = m_new;
+          // Row 4j + e of o[rt][m] and lsum[rt] is element e.
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a = shfl(alpha, 4 * j + e);
+            lsum[rt][e] *= a;
+#pragma unroll
+            for (int m = 0; m < CH; ++m) o[rt][m][e] *= a;
+          }
+        }
+        const float msub = m_run[rt] == kNegInf ? 0.f : m_run[rt] * c;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pf[rt][4 * h + e] = fast_exp2(__builtin_fmaf(sacc[h][rt][e], c, -msub));
+      }
+      // P's k-slot 4h + e is token 32(g%2) + 16h + 4j + e, as in pv().
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt) {
+        if constexpr (!EXACT) {
+          pa[rt] = pack8<_Float16>(pf[rt]);
+        } else {
+          // P split into its bf16 value and bf16 residual.
+          float lo[8];
+          pa[rt] = pack8<__bf16>(pf[rt]);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) lo[k] = pf[rt][k] - (float)pa[rt][k];
+          pl[rt] = pack8<__bf16>(lo);
+        }
+      }
+    };
+    auto softmax_step = [&](int g, bool full) { softmax(g, full); };
+    auto tile_full = [&](int tile) {
+      return __all(sValid[tile % 3][lane] != 0) && tile * kBK + kBK - 1 <= wave_lim;
+    };
+
     if (tid == 0) sOvf = 0;
     fetch_blocks(0);
     if (ntiles > 0) {
@@ -244,144 +390,33 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     }
     __syncthreads();
 
+    const bool lag = wave >= kWaves / 2;  // softmax one step behind
+    bool full_prev = false;
     for (int tile = 0; tile < ntiles; ++tile) {
-      const int buf = tile & 1;
       const bool more = tile + 1 < ntiles;
       if (more) {
         load_tile(tile + 1);     // block ids fetched last iteration
         fetch_blocks(tile + 2);  // block-table entries for the tile after
       }
-      const T *K = sK[buf];
-      const int t0 = tile * kBK;
+      const bool full = tile_full(tile);
+      const int g = 2 * tile;
+      if (lag && tile > 0) softmax_step(g - 1, full_prev);
+      qk(g);
+      if (tile > 0) pv(g - 1);
+      softmax_step(g, full);
+      qk(g + 1);
+      pv(g);
+      if (!lag) softmax_step(g + 1, full);
+      full_prev = full;
 
-      // full: every token of the tile is readable and visible to every row of
-      // this wave, so no per-element mask is needed.
-      const bool all_valid = __all(sValid[buf][lane] != 0);
-      const bool full = all_valid && t0 + kBK - 1 <= wave_lim;
-
-      // The tile is processed in two 32-token halves: scores, softmax, P.V.
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        // ---- scores: sacc[h][rt][e] = S'[row 16rt + n16][token t0 + 32half + 16h + 4j + e]
-        f32x4 sacc[2][kRT];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int rt = 0; rt < kRT; ++rt) sacc[h][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int i = 0; i < NQK; ++i) {
-            const qk_t a = __builtin_bit_cast(
-                qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * KROW + 32 * i + 8 * j]));
-#pragma unroll
-            for (int rt = 0; rt < kRT; ++rt)
-              sacc[h][rt] = MfQK::run(a, __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
-          }
-        }
-
-        // ---- online softmax
-        float pf[kRT][8];
-#pragma unroll
-        for (int rt = 0; rt < kRT; ++rt) {
-          float mx = kNegInf;
-          if (full) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sacc[h][rt][e]);
-          } else {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const uint32_t vf =
-                  *reinterpret_cast<const uint32_t *>(&sValid[buf][32 * half + 16 * h + 4 * j]);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int pos = t0 + 32 * half + 16 * h + 4 * j + e;
-                const bool ok = ((vf >> (8 * e)) & 0xffu) != 0 && pos <= lim[rt];
-                if (!ok) sacc[h][rt][e] = kNegInf;
-                mx = fmaxf(mx, sacc[h][rt][e]);
-              }
-            }
-          }
-          mx = fmaxf(mx, shfl_xor(mx, 16));
-          mx = fmaxf(mx, shfl_xor(mx, 32));
-          // Raise the running max only when the scores exceed it by > 2^8 (or
-          // it is still -inf); c == 0 never rescales (every p is 1).
-          const bool grow = (mx - m_run[rt]) * c > kRescaleLog2;
-          if (__any(grow)) {
-            const float m_new = fmaxf(m_run[rt], mx);
-            // 0 when the row had no visible token yet, 1 if its max is unchanged.
-            const float alpha = m_new == kNegInf ? 1.f : fast_exp2((m_run[rt] - m_new) * c);
-            m_run[rt] = m_new;
-            l_run[rt] *= alpha;
-            // Row 4j + e of o[rt][m] is element e.
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float a = shfl(alpha, 4 * j + e);
-#pragma unroll
-              for (int m = 0; m < CH; ++m) o[rt][m][e] *= a;
-            }
-          }
-          const float msub = m_run[rt] == kNegInf ? 0.f : m_run[rt] * c;
-          float psum = 0.f;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float x = sacc[h][rt][e];
-              float pr = fast_exp2(__builtin_fmaf(x, c, -msub));
-              if (!full) pr = x == kNegInf ? 0.f : pr;
-              pf[rt][4 * h + e] = pr;
-              psum += pr;
-            }
-          }
-          l_run[rt] += psum;
-        }
-
-        // ---- O += P V over the half's 32 tokens. P's k-slot 4h + e and V's
-        // row chunk vr[4h + e] are both token 32half + 16h + 4j + e; MFMA m
-        // produces output columns d = n16 * CH + m.
-        // B operand of MFMA m (output columns d = 16m + n16): lane (n16, j)
-        // needs V[token of k-slot 4h + kk][16m + n16], two transposed LDS
-        // reads (h = 0, 1) of four tokens each (see vt_read).
-        const uint16_t *vrow = &sV[buf][(32 * half + 4 * j + (n16 >> 2)) * VROW + 4 * (n16 & 3)];
-        if constexpr (!EXACT) {
-          pv_t pa[kRT];
-#pragma unroll
-          for (int rt = 0; rt < kRT; ++rt) pa[rt] = pack8<_Float16>(pf[rt]);
-#pragma unroll
-          for (int m = 0; m < CH; ++m) {
-            const pv_t vb = __builtin_bit_cast(pv_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
-#pragma unroll
-            for (int rt = 0; rt < kRT; ++rt) o[rt][m] = MfPV::run(pa[rt], vb, o[rt][m]);
-          }
-        } else {
-          // bf16 V, P split into its bf16 value and bf16 residual.
-          typedef Mfma16x16x32<__bf16> MfB;
-          typedef typename MfB::op_t b_t;
-          b_t pa[kRT], pl[kRT];
-#pragma unroll
-          for (int rt = 0; rt < kRT; ++rt) {
-            float lo[8];
-            pa[rt] = pack8<__bf16>(pf[rt]);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) lo[k] = pf[rt][k] - (float)pa[rt][k];
-            pl[rt] = pack8<__bf16>(lo);
-          }
-#pragma unroll
-          for (int m = 0; m < CH; ++m) {
-            const b_t vb = __builtin_bit_cast(b_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
-#pragma unroll
-            for (int rt = 0; rt < kRT; ++rt) {
-              o[rt][m] = MfB::run(pa[rt], vb, o[rt][m]);
-              o[rt][m] = MfB::run(pl[rt], vb, o[rt][m]);
-            }
-          }
-        }
-      }
-
-      if (more) store_tile(buf ^ 1, exact_c);
+      if (more) store_tile((tile + 1) % 3, exact_c);
       __syncthreads();
     }
+    if (ntiles > 0) {
+      if (lag) softmax_step(2 * ntiles - 1, full_prev);
+      pv(2 * ntiles - 1);
+    }
+    __syncthreads();  // sOvf final; LDS free for a second pass
     return kBf16 && !EXACT && sOvf != 0;
   };
 
@@ -393,11 +428,9 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   // ---- normalise and store rows 32w + 16rt + 4j + e
 #pragma unroll
   for (int rt = 0; rt < kRT; ++rt) {
-    l_run[rt] += shfl_xor(l_run[rt], 16);
-    l_run[rt] += shfl_xor(l_run[rt], 32);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float l = shfl(l_run[rt], 4 * j + e);
+      const float l = lsum[rt][e];
       const int row = 32 * wave + 16 * rt + 4 * j + e;
       const int tok = q0 + row / G;
       if (row >= bq * G || tok >= n_new) continue;

@@ -270,7 +270,7 @@ int stream_depth_setting() {
     const int d = atoi(env);
     if (d == 2 || d == 3 || d == 4 || d == 6) return d;
   }
-  return 4;
+  return 3;
 }
 
 // Validates a balanced-decode call and lays the workspace out in p.

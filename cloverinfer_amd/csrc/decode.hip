@@ -159,43 +159,19 @@ __global__ void __launch_bounds__(NW * 64) paged_decode_valu(const DecodeParams 
 // One wave per (sequence, query head). Restates the partial-softmax merge of
 // src/core/resident_kv_store.py:2497-2509 over all partitions at once:
 //   M = max_i m_i,  w_i = l_i e^{m_i - M},  out = sum_i c_i w_i / max(sum_i w_i, 1e-12).
+// One workgroup (4 waves) per (sequence, query head): the partitions' partials
+// are merged by lse_merge.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) splitk_reduce(const DecodeParams p) {
-  constexpr int EPL = (D + 63) / 64;  // elements per lane (lanes >= D idle when D < 64)
-  const int lane = threadIdx.x & 63;
-  const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (idx >= (int64_t)p.num_seqs * p.num_heads) return;
+  __shared__ float smem[4 * (D + 1)];
+  const int64_t idx = blockIdx.x;
   const int s = (int)(idx / p.num_heads);
   const int h = (int)(idx - (int64_t)s * p.num_heads);
   const int ctx = clamp_ctx(p, s);
   const int nparts = (ctx + p.partition_size - 1) / p.partition_size;
   const int64_t row0 = idx * p.max_parts;
-  const float *wm = p.ws_m + row0;
-  const float *wl = p.ws_l + row0;
-  const float *wo = p.ws_o + row0 * D;
-
-  float M = kNegInf;
-  for (int i = lane; i < nparts; i += 64) M = fmaxf(M, wm[i]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-  const float Msub = (M == kNegInf) ? 0.f : M;
-
-  float L = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int i = 0; i < nparts; ++i) {
-    const float w = wl[i] * fast_exp2((wm[i] - Msub) * kLog2e);
-    L += w;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e)
-      if (lane + 64 * e < D) acc[e] += wo[(int64_t)i * D + lane + 64 * e] * w;
-  }
-  const float inv = 1.f / fmaxf(L, 1e-12f);
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e)
-    if (lane + 64 * e < D) dst[lane + 64 * e] = from_f32<T>(acc[e] * inv);
+  lse_merge<T, D, 4>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 1, D, nparts, dst, smem);
 }
 
 template <typename T, int D>
@@ -251,7 +227,9 @@ hipError_t launch_valu_t(const DecodeParams &p, hipStream_t stream) {
 template <typename T>
 hipError_t launch_reduce_t(const DecodeParams &p, hipStream_t stream) {
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (rows <= 0) return hipSuccess;
+  if (rows > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)rows);
   switch (p.head_dim) {
     case 8: hipLaunchKernelGGL((splitk_reduce<T, 8>), grid, dim3(256), 0, stream, p); break;
     case 16: hipLaunchKernelGGL((splitk_reduce<T, 16>), grid, dim3(256), 0, stream, p); break;

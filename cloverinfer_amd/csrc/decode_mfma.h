@@ -123,14 +123,40 @@ struct DecodeWave {
   // number of loads in flight never depends on the lane mask.
   __device__ __forceinline__ void load_q(const DecodeParams &p, int s, int h0, int ng,
                                          qk_t (&q)[NQK]) const {
+    u32x4 raw[NQK];
+    load_q_raw(p, s, h0, ng, raw);
+    mask_q(raw, ng, q);
+  }
+
+  // The two halves of load_q, for callers that prefetch: the loads, and the
+  // zeroing of rows >= ng (which waits for them).
+  __device__ __forceinline__ void load_q_raw(const DecodeParams &p, int s, int h0, int ng,
+                                             u32x4 (&raw)[NQK]) const {
     const int row = min(n16, ng - 1);
     const T *qrow = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)(h0 + row) * p.q_stride_head;
 #pragma unroll
-    for (int i = 0; i < NQK; ++i) {
-      u32x4 w = load_vec<u32x4>(qrow + 32 * i + 8 * j);
-      if (n16 >= ng) w = (u32x4){0u, 0u, 0u, 0u};
-      q[i] = __builtin_bit_cast(qk_t, w);
-    }
+    for (int i = 0; i < NQK; ++i) raw[i] = load_vec<u32x4>(qrow + 32 * i + 8 * j);
+  }
+  __device__ __forceinline__ void mask_q(const u32x4 (&raw)[NQK], int ng, qk_t (&q)[NQK]) const {
+#pragma unroll
+    for (int i = 0; i < NQK; ++i)
+      q[i] = __builtin_bit_cast(qk_t, n16 < ng ? raw[i] : (u32x4){0u, 0u, 0u, 0u});
+  }
+
+  // UNI: issue the loads of the 16-token step at token `tok` of block `blk`
+  // of a kv head whose pools start at kbase / vbase. A block id outside
+  // [0, num_blocks) reads a readable row and is masked when computed.
+  __device__ __forceinline__ void issue_blk(const char *kbase, const char *vbase, int blk, int tok,
+                                            Regs &R) const {
+    const bool ok = (unsigned)blk < nblocks;
+    const int64_t off = ok ? blk * sblk + tok * stok : 0;
+    R.ok = ok;
+    const rsrc_t rk = make_rsrc(kbase + off);
+    const rsrc_t rv = make_rsrc(vbase + off);
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4, kCacheDefault>(rk, k_lane + 64u * i);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t, kCacheStream>(rv, v_lane[r]);
   }
 
   // Issue every load of the step starting at token `base` (< g.t_end). All
@@ -138,16 +164,7 @@ struct DecodeWave {
   // readable row and are masked when the step is computed.
   __device__ __forceinline__ void issue(const SegGeom &g, int base, Regs &R) const {
     if constexpr (UNI) {
-      const int blk = scalar_load_i32(g.bt + (base >> bshift));
-      const bool ok = (unsigned)blk < nblocks;
-      const int64_t off = ok ? blk * sblk + (base & bmask) * stok : 0;
-      R.ok = ok;
-      const rsrc_t rk = make_rsrc(g.kbase + off);
-      const rsrc_t rv = make_rsrc(g.vbase + off);
-#pragma unroll
-      for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4, kCacheDefault>(rk, k_lane + 64u * i);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) R.v[r] = buf_load<vchunk_t, kCacheStream>(rv, v_lane[r]);
+      issue_blk(g.kbase, g.vbase, scalar_load_i32(g.bt + (base >> bshift)), base & bmask, R);
     } else {
       const int tk = base + n16;
       const int kb = tk < g.t_end ? g.bt[tk >> bshift] : 0;
@@ -254,5 +271,103 @@ struct DecodeWave {
     }
   }
 };
+
+// Log-sum-exp merge of n partial rows, the rule of the reference's
+// partial-softmax merge (src/core/resident_kv_store.py:2497-2509) over all
+// rows at once:
+//   M = max_i m_i, w_i = l_i e^(m_i - M), out = sum_i c_i w_i / max(sum_i w_i, 1e-12).
+// Row i: row max m[i * ms] (natural-log domain), row sum l[i * ms], context
+// c[i * cs .. + D]. NW waves (consecutive in the workgroup, NW > 1 only for a
+// one-row workgroup) split the rows 64 at a time; each lane weighs one row of
+// a 64-row chunk, and eight context rows are loaded per round so that their
+// latencies overlap. NW > 1 combines the waves through smem (NW * (D + 1)
+// floats) and needs every thread of the workgroup to call this.
+template <typename T, int D, int NW>
+__device__ __forceinline__ void lse_merge(const float *m, const float *l, const float *c,
+                                          int64_t ms, int64_t cs, int n, T *dst, float *smem) {
+  constexpr int EPL = (D + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  const int wv = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+  // The row's max needs every m_i; the first chunk's (m, l) and its first
+  // eight context rows are loaded together, before any reduction, so that a
+  // row with at most 64 partials costs one round trip to memory.
+  const int base0 = 64 * wv;
+  const int cnt0 = max(0, min(64, n - base0));
+  float m0 = kNegInf, l0 = 0.f;
+  if (lane < cnt0) {
+    m0 = m[(int64_t)(base0 + lane) * ms];
+    l0 = l[(int64_t)(base0 + lane) * ms];
+  }
+  float v[8][EPL];
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      v[u][e] = (u < cnt0 && lane + 64 * e < D) ? c[(int64_t)(base0 + u) * cs + lane + 64 * e] : 0.f;
+  float M = m0;
+  for (int i = lane; i < n; i += 64)
+    if (i < base0 || i >= base0 + 64) M = fmaxf(M, m[i * ms]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+  const float Msub = (M == kNegInf) ? 0.f : M;
+  float L = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  for (int base = base0; base < n; base += 64 * NW) {
+    const int cnt = min(64, n - base);
+    float wl = 0.f;
+    if (base == base0) {
+      if (lane < cnt) wl = l0 * fast_exp2((m0 - Msub) * kLog2e);
+    } else if (lane < cnt) {
+      const int64_t r = (int64_t)(base + lane) * ms;
+      wl = l[r] * fast_exp2((m[r] - Msub) * kLog2e);
+    }
+    L += wl;
+    for (int k = 0; k < cnt; k += 8) {
+      if (base != base0 || k != 0) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int e = 0; e < EPL; ++e)
+            v[u][e] = (k + u < cnt && lane + 64 * e < D)
+                          ? c[(int64_t)(base + k + u) * cs + lane + 64 * e] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = __builtin_bit_cast(
+            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k + u < 64 ? k + u : 63));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] += v[u][e] * w;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) L += shfl_xor(L, off);
+  if constexpr (NW > 1) {
+    float *sl = smem;
+    float *sa = smem + NW;
+    if (lane == 0) sl[wv] = L;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+      if (lane + 64 * e < D) sa[wv * D + lane + 64 * e] = acc[e];
+    __syncthreads();
+    if (wv != 0) return;
+    L = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) L += sl[w];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      acc[e] = 0.f;
+      if (lane + 64 * e < D)
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[e] += sa[w * D + lane + 64 * e];
+    }
+  }
+  const float inv = 1.f / fmaxf(L, 1e-12f);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e)
+    if (lane + 64 * e < D) dst[lane + 64 * e] = from_f32<T>(acc[e] * inv);
+}
 
 }  // namespace clv

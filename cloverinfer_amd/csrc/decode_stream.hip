@@ -8,7 +8,7 @@
 // evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders
 // (W is capped at N, so no wave is idle and a segment's partials come from
 // consecutive waves).
-// Each wave keeps three steps of loads in flight and, for every segment it
+// Each wave keeps a ring of steps of loads in flight and, for every segment it
 // touches, writes one partial (normalised context, row max, row sum) to the
 // workspace; stream_reduce merges the partials of each
 // (sequence, query head) with the log-sum-exp rule of the reference's
@@ -142,14 +142,34 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     const int ng = min(16, p.group - g0);
     const int ctx = clamp_ctx(p, lens, s_);
     const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
-    qk_t q[WV::NQK];
-    w.load_q(p, s_, kvh * p.group + g0, ng, q);
+    // Q loads go out first and are waited for only after the ring below is
+    // issued, so a run start costs one memory latency, not two.
+    u32x4 qraw[WV::NQK];
+    w.load_q_raw(p, s_, kvh * p.group + g0, ng, qraw);
 
     // Ring of DEPTH register sets; past the run's last step it re-reads that
     // step (cache resident, never used).
     typename WV::Regs R[DEPTH];
+    // UNI: block-table entries are read through the constant address space
+    // (the kernel never writes the table), so the compiler issues them as
+    // scalar loads it waits for only at use; each is read one issue ahead.
+    typedef const int32_t __attribute__((address_space(4))) *cint_t;
+    const cint_t brow = (cint_t)(tables + (int64_t)s_ * p.max_blocks_per_seq);
+    auto base_of = [&](int step) { return (min(step, last) - first) * WV::STEP; };
+    int blk = 0;
+    if constexpr (UNI) blk = brow[base_of(x) >> p.block_shift];
+    auto issue = [&](int step, typename WV::Regs &Rg) {
+      if constexpr (UNI) {
+        w.issue_blk(geo.kbase, geo.vbase, blk, base_of(step) & w.bmask, Rg);
+        blk = brow[base_of(step + 1) >> p.block_shift];
+      } else {
+        w.issue(geo, base_of(step), Rg);
+      }
+    };
 #pragma unroll
-    for (int i = 0; i < DEPTH; ++i) w.issue(geo, (min(x + i, last) - first) * WV::STEP, R[i]);
+    for (int i = 0; i < DEPTH; ++i) issue(x + i, R[i]);
+    qk_t q[WV::NQK];
+    w.mask_q(qraw, ng, q);
     int c = x;
     bool done = false;
     while (!done) {
@@ -160,7 +180,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
           if (++c > last)
             done = true;
           else
-            w.issue(geo, (min(c + DEPTH - 1, last) - first) * WV::STEP, R[i]);
+            issue(c + DEPTH - 1, R[i]);
         }
       }
     }
@@ -172,37 +192,6 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     w.reset();
     x = last + 1;
   }
-}
-
-// Merge n partial rows (row i at index i * stride of wm/wl and i * stride * D
-// of wo) into dst, as src/core/resident_kv_store.py:2497-2509 does pairwise:
-//   M = max_i m_i, w_i = l_i e^{m_i - M}, out = sum_i c_i w_i / max(sum_i w_i, 1e-12).
-template <typename T, int D>
-__device__ __forceinline__ void merge_partials(const float *wm, const float *wl, const float *wo,
-                                               int64_t stride, int n, T *dst) {
-  constexpr int EPL = (D + 63) / 64;
-  const int lane = threadIdx.x & 63;
-  float M = kNegInf;
-  for (int i = lane; i < n; i += 64) M = fmaxf(M, wm[(int64_t)i * stride]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-  const float Msub = (M == kNegInf) ? 0.f : M;
-  float L = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int i = 0; i < n; ++i) {
-    const int64_t r = (int64_t)i * stride;
-    const float wt = wl[r] * fast_exp2((wm[r] - Msub) * kLog2e);
-    L += wt;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e)
-      if (lane + 64 * e < D) acc[e] += wo[r * D + lane + 64 * e] * wt;
-  }
-  const float inv = 1.f / fmaxf(L, 1e-12f);
-#pragma unroll
-  for (int e = 0; e < EPL; ++e)
-    if (lane + 64 * e < D) dst[lane + 64 * e] = from_f32<T>(acc[e] * inv);
 }
 
 // One wave per (sequence, query head).
@@ -223,7 +212,7 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
   const int64_t row0 = (int64_t)p.slot_prefix[seg] * 16 + g;
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
-  merge_partials<T, D>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16, n, dst);
+  lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16, 16 * D, n, dst, nullptr);
 }
 
 template <typename T, int D, int DEPTH>

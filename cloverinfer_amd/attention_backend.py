@@ -11,26 +11,35 @@ Storage is paged instead of one contiguous tensor per (request, layer):
 per-layer pools ``[num_blocks, block_size, num_kv_heads, head_dim]`` share
 one block table per request, so token p of a request lives in the same slot
 of every layer. A batch of decode items for one layer becomes one
-reshape_and_cache launch plus one paged-decode launch.
+reshape_and_cache launch plus one paged-decode launch, fed by:
+
+* a device-resident block table (``DeviceBlockTable``): a request's row is
+  written once at ``init_request``; a block taken during decode is one
+  queued entry (the reference rebuilds the table on the host every call,
+  src/core/memory_manager.py:145-173);
+* one host-to-device copy of the batch's q/k/v rows, staged in pinned
+  memory, and one of its metadata (slots, context lengths, table rows);
+* one device-to-host copy of the batch's outputs.
 """
 from __future__ import annotations
 
 import math
 from typing import Dict, List, Optional
 
-import numpy as np
 import torch
 
 from . import kernels
+from .block_table import DeviceBlockTable
 
 
 class _Request:
-    __slots__ = ("blocks", "layer_lens", "context_len")
+    __slots__ = ("blocks", "layer_lens", "context_len", "row")
 
-    def __init__(self, blocks: List[int], num_layers: int, seq_len: int):
+    def __init__(self, blocks: List[int], num_layers: int, seq_len: int, row: int):
         self.blocks = blocks
         self.layer_lens = [seq_len] * num_layers
         self.context_len = seq_len
+        self.row = row  # row of the device block table
 
 
 class GpuAttentionBackend:
@@ -50,6 +59,9 @@ class GpuAttentionBackend:
         self.num_layers = 0
         self.free_blocks: List[int] = list(range(num_blocks))
         self.requests: Dict[str, _Request] = {}
+        self.tables = DeviceBlockTable(self.device)
+        self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
+        self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
         self.stats = {"decode_items": 0, "decode_launches": 0, "init_requests": 0}
 
     # ------------------------------------------------------------ pools
@@ -91,8 +103,8 @@ class GpuAttentionBackend:
         self._ensure_pools(len(initial_kv), hkv, d, k0.dtype)
         reserve = max(1, int(decode_reserve_tokens))
         nblocks = max(1, math.ceil((seq_len + reserve) / self.block_size))
-        req = _Request(self._take_blocks(nblocks, "OOM: Not enough blocks"), self.num_layers,
-                       seq_len)
+        blocks = self._take_blocks(nblocks, "OOM: Not enough blocks")
+        req = _Request(blocks, self.num_layers, seq_len, self.tables.add(blocks))
         if seq_len:
             slots = torch.tensor([self._slot(req, p) for p in range(seq_len)],
                                  dtype=torch.int64).to(self.device)
@@ -101,6 +113,7 @@ class GpuAttentionBackend:
                 v = kv["value"].to(device=self.device, dtype=self.v_pools.dtype)
                 if k.shape != (seq_len, hkv, d) or v.shape != k.shape:
                     self.free_blocks.extend(req.blocks)
+                    self.tables.remove(req.row)
                     raise ValueError(f"layer {layer}: key/value shape differs from layer 0")
                 kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots)
         self.requests[request_id] = req
@@ -120,67 +133,118 @@ class GpuAttentionBackend:
         requests form one launch pair (append + decode)."""
         out: List[torch.Tensor] = []
         wave: List[Dict[str, object]] = []
+        in_wave = set()
         key = None
         for it in items:
             rid = str(it["request_id"])
             if rid not in self.requests:
                 raise KeyError(f"Unknown request {rid}")
             k = (int(it["layer_idx"]), float(it.get("score_scale", 1.0)))
-            if wave and (k != key or any(str(w["request_id"]) == rid for w in wave)):
+            if wave and (k != key or rid in in_wave):
                 out.extend(self._run_wave(wave, *key))
                 wave = []
+                in_wave = set()
             key = k
             wave.append(it)
+            in_wave.add(rid)
         if wave:
             out.extend(self._run_wave(wave, *key))
         return out
+
+    def _staging(self, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
+        """A pinned host buffer of at least ``shape``, reused across calls (the
+        caller waits for the previous call's copies out of it first)."""
+        n = 1
+        for x in shape:
+            n *= x
+        buf = self._stage.get(name)
+        if buf is None or buf.dtype != dtype or buf.numel() < n:
+            buf = torch.empty(max(n, 1), dtype=dtype, pin_memory=True)
+            self._stage[name] = buf
+        return buf[:n].view(*shape)
+
+    def _rows(self, items: List[Dict[str, object]], name: str, heads: int, d: int,
+              dt: torch.dtype) -> torch.Tensor:
+        """The items' ``name`` tensors ([heads, d] or [1, heads, d]) as one
+        device tensor [B, heads, d], through one copy."""
+        ts = [it[name] for it in items]
+        n = len(ts)
+        shape = ts[0].shape
+        same = all(t.shape == shape for t in ts) and ts[0].numel() == heads * d
+        if same and all(t.device == self.device for t in ts):
+            return torch.stack(ts).view(n, heads, d).to(dt)
+        host = self._staging(name, (n, heads, d), dt)
+        if same and all(t.dtype == dt and t.device.type == "cpu" for t in ts):
+            torch.stack(ts, out=host.view(n, *shape))
+        else:
+            host.copy_(torch.stack([t.reshape(heads, d).to("cpu") for t in ts]))
+        return host.to(self.device, non_blocking=True)
 
     def _run_wave(self, items: List[Dict[str, object]], layer: int,
                   score_scale: float) -> List[torch.Tensor]:
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"layer_idx {layer} outside [0, {self.num_layers})")
         dt = self.k_pools.dtype
+        _, _, bs, hkv, d = self.k_pools.shape
+        if self._stage_done is not None:
+            self._stage_done.synchronize()  # the staging buffers are free again
+        q0 = items[0]["query"]
+        hq = q0.numel() // d
+        n = len(items)
+        q = self._rows(items, "query", hq, d, dt)
+        k = self._rows(items, "key", hkv, d, dt)
+        v = self._rows(items, "value", hkv, d, dt)
 
-        def rows(name: str) -> torch.Tensor:
-            ts = []
-            for it in items:
-                t = it[name]
-                ts.append(t.squeeze(0) if t.dim() == 3 else t)
-            return torch.stack(ts).to(device=self.device, dtype=dt)
-
-        q, k, v = rows("query"), rows("key"), rows("value")
+        # Metadata, one copy: slots (int64), new block-table entries (int64
+        # rows / columns / blocks), context lengths and table rows (int32).
         reqs = [self.requests[str(it["request_id"])] for it in items]
-        slots = []
+        slots, lens, rows = [], [], []
         for req in reqs:
             pos = req.layer_lens[layer]
-            if pos >= len(req.blocks) * self.block_size:
-                req.blocks.extend(self._take_blocks(1, "OOM during append"))
-            slots.append(self._slot(req, pos))
-        kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer],
-                                  torch.tensor(slots, dtype=torch.int64).to(self.device))
-        for req in reqs:
-            req.layer_lens[layer] += 1
-        lens = [req.layer_lens[layer] for req in reqs]
-        width = max(len(req.blocks) for req in reqs)
-        table = np.full((len(reqs), width), -1, dtype=np.int32)
-        for i, req in enumerate(reqs):
-            table[i, :len(req.blocks)] = req.blocks
-        bt = torch.from_numpy(table).to(self.device)
-        ctx = torch.tensor(lens, dtype=torch.int32).to(self.device)
+            if pos >= len(req.blocks) * bs:
+                blk = self._take_blocks(1, "OOM during append")[0]
+                self.tables.set(req.row, len(req.blocks), blk)
+                req.blocks.append(blk)
+            slots.append(req.blocks[pos // bs] * bs + pos % bs)
+            req.layer_lens[layer] = pos + 1
+            lens.append(pos + 1)
+            rows.append(req.row)
+        upd = self.tables.take_pending()
+        nu = len(upd)
+        meta = self._staging("meta", (4 * n + 6 * nu,), torch.int32)
+        wide = [*slots]
+        for part in range(3):
+            wide.extend(u[part] for u in upd)
+        meta[:2 * (n + 3 * nu)].view(torch.int64).copy_(torch.tensor(wide, dtype=torch.int64))
+        meta[2 * (n + 3 * nu):].copy_(torch.tensor(lens + rows, dtype=torch.int32))
+        meta_dev = meta.to(self.device, non_blocking=True)
+        self._stage_done = torch.cuda.Event()
+        self._stage_done.record()
+        wide_dev = meta_dev[:2 * (n + 3 * nu)].view(torch.int64)
+        if nu:
+            self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
+        slots_dev = wide_dev[:n]
+        ctx_dev = meta_dev[2 * (n + 3 * nu):2 * (n + 3 * nu) + n]
+        kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots_dev)
+        bt = self.tables.rows(rows, meta_dev[2 * (n + 3 * nu) + n:])
         ctx_out = torch.empty_like(q)
-        kernels.paged_attention(ctx_out, q, self.k_pools[layer], self.v_pools[layer], bt, ctx,
-                                self.block_size, max(lens), scale=score_scale,
+        kernels.paged_attention(ctx_out, q, self.k_pools[layer], self.v_pools[layer], bt,
+                                ctx_dev, bs, max(lens), scale=score_scale,
                                 partition_size=self.partition_size)
         if layer == self.num_layers - 1:
             for req in reqs:
                 req.context_len += 1
-        self.stats["decode_items"] += len(items)
+        self.stats["decode_items"] += n
         self.stats["decode_launches"] += 1
-        results = []
-        for i, it in enumerate(items):
-            qin = it["query"]
-            results.append(ctx_out[i].unsqueeze(0).to(device=qin.device, dtype=qin.dtype))
-        return results
+        # Outputs in each query's dtype and on its device: one copy for the
+        # batch when the queries agree (the node's case), per item otherwise.
+        want = {(it["query"].device, it["query"].dtype) for it in items}
+        if len(want) == 1:
+            dev, qdt = want.pop()
+            res = ctx_out.to(device=dev, dtype=qdt)
+            return [res[i:i + 1] for i in range(n)]
+        return [ctx_out[i:i + 1].to(device=it["query"].device, dtype=it["query"].dtype)
+                for i, it in enumerate(items)]
 
     def get_context_len(self, request_id: str) -> int:
         return self.requests[request_id].context_len
@@ -189,6 +253,7 @@ class GpuAttentionBackend:
         req = self.requests.pop(request_id, None)
         if req is not None:
             self.free_blocks.extend(req.blocks)
+            self.tables.remove(req.row)
 
     def get_debug_info(self) -> Dict[str, object]:
         return {

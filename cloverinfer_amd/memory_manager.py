@@ -11,7 +11,11 @@ padding. Additive only:
   query heads share them with the repeat_kv grouping;
 * ``scale`` (default 1/sqrt(head_dim), the reference kernel's constant);
 * bfloat16 pools;
-* ``write_new_kv_batch`` and ``slot_mapping`` (one device launch for a batch).
+* ``write_new_kv_batch`` and ``slot_mapping`` (one device launch for a batch);
+* on a HIP device, ``attention`` reads a device-resident mirror of the block
+  tables that allocate / append_slot / free keep up to date (one row write
+  per request, one entry per new block) instead of the per-call host build
+  that ``get_kernel_inputs`` keeps for callers that want the tensors.
 
 Data movement and attention always run the HIP kernels through the C ABI;
 on a CPU device the bookkeeping works but the data path raises.
@@ -25,6 +29,7 @@ import numpy as np
 import torch
 
 from . import kernels
+from .block_table import DeviceBlockTable
 
 
 class KVCacheManager:
@@ -52,6 +57,10 @@ class KVCacheManager:
         self.free_blocks: List[int] = list(range(num_blocks))
         self.block_tables: Dict[str, List[int]] = {}
         self.context_lens: Dict[str, int] = {}
+        # Device mirror of block_tables for attention() (HIP pools only).
+        self._dev_tables: Optional[DeviceBlockTable] = (
+            DeviceBlockTable(torch.device(device)) if torch.device(device).type == "cuda" else None)
+        self._dev_rows: Dict[str, int] = {}
 
     # ------------------------------------------------------------ bookkeeping
     def allocate(self, request_id: str, seq_len: int = 0) -> None:
@@ -63,6 +72,8 @@ class KVCacheManager:
             raise RuntimeError("OOM: Not enough blocks")
         self.block_tables[request_id] = [self.free_blocks.pop() for _ in range(required)]
         self.context_lens[request_id] = seq_len
+        if self._dev_tables is not None:
+            self._dev_rows[request_id] = self._dev_tables.add(self.block_tables[request_id])
 
     def append_slot(self, request_id: str):
         """Advance the context by one token, taking a new block when the
@@ -74,6 +85,8 @@ class KVCacheManager:
             if not self.free_blocks:
                 raise RuntimeError("OOM during append")
             blocks.append(self.free_blocks.pop())
+            if self._dev_tables is not None:
+                self._dev_tables.set(self._dev_rows[request_id], len(blocks) - 1, blocks[-1])
         self.context_lens[request_id] = current + 1
         return blocks[current // self.block_size], current % self.block_size
 
@@ -84,6 +97,8 @@ class KVCacheManager:
             return
         self.free_blocks.extend(blocks)
         del self.context_lens[request_id]
+        if self._dev_tables is not None:
+            self._dev_tables.remove(self._dev_rows.pop(request_id))
 
     def slot_mapping(self, request_id: str, positions: Sequence[int]) -> List[int]:
         """Cache slots (block * block_size + offset) of token positions."""
@@ -161,7 +176,10 @@ class KVCacheManager:
                   partition_size: Optional[int] = None) -> torch.Tensor:
         """Paged decode for ``q [num_seqs, num_heads, head_dim]`` (memory_manager.py:175-190)."""
         self._require_gpu("attention")
-        block_tables, ctx_lens, max_len = self.get_kernel_inputs(request_ids)
+        lens = [self.context_lens[r] for r in request_ids]
+        block_tables = self._dev_tables.rows([self._dev_rows[r] for r in request_ids])
+        ctx_lens = torch.tensor(lens, dtype=torch.int32).to(self.device)
+        max_len = max(lens, default=0)
         q = q.to(device=self.device, dtype=self.dtype)
         if not q.is_contiguous():
             q = q.contiguous()

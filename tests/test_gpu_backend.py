@@ -78,3 +78,46 @@ def test_protocol_errors():
         gpu.init_request("big", [{"key": torch.randn(200, 2, 64), "value": torch.randn(200, 2, 64)}])
     with pytest.raises(ValueError):
         create_attention_backend("cpu")
+
+
+def test_row_reuse_and_shuffled_batches():
+    """Requests freed and re-created (their device-table rows are reused),
+    batches in shuffled order (the table is gathered, not sliced), contexts
+    growing across block borders; every step against the restated
+    CpuAttentionBackend."""
+    g = torch.Generator().manual_seed(31)
+    hq, hkv, d, dtype = 8, 2, 64, torch.bfloat16
+    gpu = GpuAttentionBackend(num_blocks=256, block_size=16)
+    cpu = CpuAttentionOracle()
+    live = []
+    next_id = 0
+
+    def new_request(T):
+        nonlocal next_id
+        rid = f"r{next_id}"
+        next_id += 1
+        kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(T, hkv, d, generator=g).to(dtype)}]
+        assert gpu.init_request(rid, kv) == cpu.init_request(rid, kv) == T
+        live.append(rid)
+
+    for T in (3, 15, 16, 40, 0, 70):
+        new_request(T)
+    for step in range(40):
+        if step % 9 == 4:  # free two requests, start three (rows reused)
+            for rid in (live[1], live[3]):
+                gpu.free_request(rid)
+                cpu.free_request(rid)
+                live.remove(rid)
+            for T in (1, 33, 17):
+                new_request(T)
+        order = torch.randperm(len(live), generator=g).tolist()
+        items = [{"request_id": live[i], "layer_idx": 0,
+                  "query": torch.randn(1, hq, d, generator=g).to(dtype),
+                  "key": torch.randn(1, hkv, d, generator=g).to(dtype),
+                  "value": torch.randn(1, hkv, d, generator=g).to(dtype),
+                  "score_scale": d ** -0.5} for i in order]
+        for a, b in zip(gpu.decode_layer_batch(items), cpu.decode_layer_batch(items)):
+            assert_attention_close(a, b, what=f"step {step}")
+    for rid in live:
+        assert gpu.get_context_len(rid) == cpu.get_context_len(rid)

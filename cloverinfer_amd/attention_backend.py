@@ -120,6 +120,74 @@ class GpuAttentionBackend:
         self.stats["init_requests"] += 1
         return seq_len
 
+    def init_request_from_hf(self, request_id: str, past_key_values, layout: str = "bhtd",
+                             batch_index: int = 0, seq_len: Optional[int] = None,
+                             decode_reserve_tokens: int = 0) -> int:
+        """``init_request`` straight from a Hugging Face cache: no permute,
+        no contiguous copy, no host round trip (the reference normalises every
+        layer to a contiguous ``[T, heads, D]`` CPU tensor first,
+        src/core/model_adapter.py:174-182, 205-240).
+
+        ``past_key_values``: one entry per layer, a ``(key, value)`` pair or an
+        object with ``key_cache``/``value_cache`` or ``keys``/``values``;
+        tensors ``[B, H, T, D]`` (``layout="bhtd"``, the common one) or
+        ``[B, T, H, D]`` (``"bthd"``). Sequence ``batch_index`` is ingested,
+        its first ``seq_len`` tokens (default: all T). Each layer is one strided
+        reshape_and_cache launch into the shared block table's slots.
+        """
+        if request_id in self.requests:
+            raise ValueError(f"Request {request_id} already exists")
+        if layout not in ("bhtd", "bthd"):
+            raise ValueError(f"layout must be 'bhtd' or 'bthd', got {layout!r}")
+
+        def pair(entry):
+            for a, b in (("key_cache", "value_cache"), ("keys", "values")):
+                if hasattr(entry, a) and hasattr(entry, b):
+                    return getattr(entry, a), getattr(entry, b)
+            return entry[0], entry[1]
+
+        layers = [pair(e) for e in past_key_values]
+        if not layers:
+            raise ValueError("past_key_values must contain at least one layer")
+        views = []
+        for li, (k, v) in enumerate(layers):
+            if k.dim() != 4 or v.shape != k.shape:
+                raise ValueError(f"layer {li}: expected 4-D key/value of one shape")
+            k, v = k[batch_index], v[batch_index]
+            if layout == "bhtd":  # [H, T, D] -> [T, H, D] view
+                k, v = k.transpose(0, 1), v.transpose(0, 1)
+            views.append((k, v))
+        total, hkv, d = views[0][0].shape
+        T = total if seq_len is None else int(seq_len)
+        if not 0 <= T <= total:
+            raise ValueError(f"seq_len {T} outside [0, {total}]")
+        dt = self.kv_dtype or views[0][0].dtype
+        self._ensure_pools(len(views), hkv, d, dt)
+        reserve = max(1, int(decode_reserve_tokens))
+        nblocks = max(1, math.ceil((T + reserve) / self.block_size))
+        blocks = self._take_blocks(nblocks, "OOM: Not enough blocks")
+        req = _Request(blocks, self.num_layers, T, self.tables.add(blocks))
+        if T:
+            bs = self.block_size
+            pos = torch.arange(T)
+            slots = (torch.tensor(blocks, dtype=torch.int64)[pos // bs] * bs + pos % bs).to(
+                self.device)
+            for layer, (k, v) in enumerate(views):
+                if k.shape[1:] != (hkv, d):
+                    self.free_blocks.extend(blocks)
+                    self.tables.remove(req.row)
+                    raise ValueError(f"layer {layer}: key/value shape differs from layer 0")
+                k = k[:T].to(device=self.device, dtype=self.k_pools.dtype)
+                v = v[:T].to(device=self.device, dtype=self.v_pools.dtype)
+                if k.stride(2) != 1:
+                    k = k.contiguous()
+                if v.stride(2) != 1:
+                    v = v.contiguous()
+                kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots)
+        self.requests[request_id] = req
+        self.stats["init_requests"] += 1
+        return T
+
     def decode_layer(self, request_id: str, layer_idx: int, query: torch.Tensor,
                      key: torch.Tensor, value: torch.Tensor,
                      score_scale: float = 1.0) -> torch.Tensor:

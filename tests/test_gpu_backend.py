@@ -121,3 +121,45 @@ def test_row_reuse_and_shuffled_batches():
             assert_attention_close(a, b, what=f"step {step}")
     for rid in live:
         assert gpu.get_context_len(rid) == cpu.get_context_len(rid)
+
+
+class _LayerCache:
+    """Stands in for one layer of a Hugging Face cache object."""
+
+    def __init__(self, k, v):
+        self.key_cache, self.value_cache = k, v
+
+
+@pytest.mark.parametrize("layout", ["bhtd", "bthd"])
+def test_init_from_hf_cache_matches_normalised_ingest(layout):
+    """HF caches ingested in place (strided views, on the device) give the
+    same pools, bit for bit, as the reference's normalised [T, H, D] path, and
+    the same decode outputs as the restated CpuAttentionBackend."""
+    g = torch.Generator().manual_seed(41)
+    layers, B, hq, hkv, d, T_pad, T = 3, 2, 8, 2, 64, 37, 29
+    dtype = torch.float16
+    shape = (B, hkv, T_pad, d) if layout == "bhtd" else (B, T_pad, hkv, d)
+    cache = [(torch.randn(shape, generator=g).to(dtype).cuda(),
+              torch.randn(shape, generator=g).to(dtype).cuda()) for _ in range(layers)]
+    hf = [_LayerCache(k, v) for k, v in cache[:2]] + [cache[2]]  # both entry forms
+
+    def normalised(t):  # the reference's _normalize_*_cache for sequence 1
+        t = t[1] if layout == "bthd" else t[1].permute(1, 0, 2)
+        return t[:T].contiguous().cpu()
+
+    initial = [{"key": normalised(k), "value": normalised(v)} for k, v in cache]
+    a = GpuAttentionBackend(num_blocks=64, block_size=16)
+    b = GpuAttentionBackend(num_blocks=64, block_size=16)
+    cpu = CpuAttentionOracle()
+    assert a.init_request_from_hf("r", hf, layout=layout, batch_index=1, seq_len=T) == T
+    assert b.init_request("r", initial) == T
+    assert cpu.init_request("r", initial) == T
+    assert torch.equal(a.k_pools, b.k_pools) and torch.equal(a.v_pools, b.v_pools)
+    for layer in range(layers):
+        it = [{"request_id": "r", "layer_idx": layer,
+               "query": torch.randn(1, hq, d, generator=g).to(dtype),
+               "key": torch.randn(1, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(1, hkv, d, generator=g).to(dtype), "score_scale": 0.125}]
+        assert_attention_close(a.decode_layer_batch(it)[0], cpu.decode_layer_batch(it)[0],
+                               what=f"layer {layer}")
+    assert a.get_context_len("r") == cpu.get_context_len("r") == T + 1

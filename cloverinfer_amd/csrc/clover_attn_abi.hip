@@ -273,6 +273,19 @@ int stream_depth_setting() {
   return 3;
 }
 
+// Phantom steps the balanced decode charges for each segment a wave starts
+// (a run start costs one memory latency, about two 16-token steps on MI355X:
+// measured per-wave durations grow by ~2.5 us per extra run).
+// CLV_STREAM_RUN_COST overrides the default for tuning.
+int stream_run_cost_setting() {
+  const char *env = getenv("CLV_STREAM_RUN_COST");
+  if (env) {
+    const int c = atoi(env);
+    if (c >= 0 && c <= 64) return c;
+  }
+  return 2;
+}
+
 // Validates a balanced-decode call and lays the workspace out in p.
 int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
                   size_t workspace_bytes, clv::DecodeParams *p) {
@@ -292,6 +305,7 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   char *ws = (char *)workspace;
   p->num_waves = num_waves;
   p->stream_depth = stream_depth_setting();
+  p->stream_run_cost = stream_run_cost_setting();
   p->num_segments = (int32_t)nseg;
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);

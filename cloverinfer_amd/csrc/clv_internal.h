@@ -36,6 +36,7 @@ struct DecodeParams {
   // ws_o/ws_m/ws_l, plus the segment prefix sums written by workgroup 0.
   int32_t num_waves;
   int32_t stream_depth;   // steps of loads each wave keeps in flight
+  int32_t stream_run_cost;  // phantom steps charged for each segment start (see decode_stream.hip)
   int32_t num_segments;   // num_seqs * num_kv_heads * n_gchunks
   int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
   int32_t *slot_prefix;   // [num_segments + 1] exclusive prefix of partials per segment

@@ -14,6 +14,12 @@
 // (sequence, query head) with the log-sum-exp rule of the reference's
 // partial-softmax merge (src/core/resident_kv_store.py:2497-2509).
 //
+// A run start (Q loads, ring refill) costs about one memory latency, so the
+// split charges every non-empty segment `stream_run_cost` phantom steps in
+// front of its real ones: a wave that starts more segments gets fewer real
+// steps. Segment i covers the flattened range [seg_prefix[i],
+// seg_prefix[i+1]), its real steps start stream_run_cost later.
+//
 // Every workgroup derives the segment prefix sums itself (in LDS) from
 // context_lens; workgroup 0 also stores them for the reduce kernel.
 #include "decode_mfma.h"
@@ -75,16 +81,20 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   // Every global pointer is a separate restrict argument: with stores to the
   // workspace inside the main loop, that is what lets the compiler keep the
   // wave-uniform block-table reads scalar loads.
-  typedef DecodeWave<T, D, UNI> WV;
+  typedef DecodeWave<T, D, UNI, UNI && D == 128> WV;
   typedef typename WV::qk_t qk_t;
+  __shared__ __attribute__((aligned(16))) char s_kt[kWaves][WV::KT_BYTES];
   __shared__ int s_seg[kStreamMaxSegments + 1];
   __shared__ int s_slot[kStreamMaxSegments + 1];
   __shared__ int s_tmp[kWaves];
 
   const int nseg = p.num_segments;
   const int per_seq = p.num_kv_heads * p.n_gchunks;
-  for (int i = threadIdx.x; i < nseg; i += kThreads)
-    s_seg[i] = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;  // per-lane index: vector read
+  const int K = p.stream_run_cost;
+  for (int i = threadIdx.x; i < nseg; i += kThreads) {
+    const int steps = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;  // vector read
+    s_seg[i] = steps > 0 ? steps + K : 0;
+  }
   __syncthreads();
   const int64_t N = block_exclusive_scan(s_seg, nseg, s_tmp);
   // At most one wave per step, so that every wave owns at least one step and
@@ -92,7 +102,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   const int64_t W = min((int64_t)p.num_waves, N);
   if (N > 0) {
     for (int i = threadIdx.x; i < nseg; i += kThreads) {
-      const int a = s_seg[i], b = s_seg[i + 1];
+      const int a = s_seg[i] + K, b = s_seg[i + 1];  // real steps of segment i
       s_slot[i] = b > a ? wave_of(b - 1, W, N) - wave_of(a, W, N) + 1 : 0;
     }
   } else {
@@ -126,6 +136,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
 
   WV w;
   w.init(p);
+  w.set_k_lds(s_kt[uni(threadIdx.x >> 6)]);
 
   // The span is cut at segment borders into runs. Each run loads its Q rows,
   // keeps DEPTH steps of loads in flight (a ring of register sets refilled
@@ -133,8 +144,13 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   int x = st;
   while (x < en) {
     while (uni(s_seg[seg + 1]) <= x) ++seg;  // skip empty segments
-    const int first = uni(s_seg[seg]);
+    const int first = uni(s_seg[seg]) + K;   // first real step
     const int last = min(en, uni(s_seg[seg + 1])) - 1;
+    if (max(x, first) > last) {  // only phantom steps of this segment
+      x = last + 1;
+      continue;
+    }
+    x = max(x, first);
     const int s_ = seg / per_seq;
     const int rem = seg - s_ * per_seq;
     const int kvh = rem / p.n_gchunks;
@@ -205,7 +221,7 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int gall = h - kvh * p.group;
   const int seg = (s * p.num_kv_heads + kvh) * p.n_gchunks + gall / 16;
   const int g = gall % 16;
-  const int a = p.seg_prefix[seg], b = p.seg_prefix[seg + 1];
+  const int a = p.seg_prefix[seg] + p.stream_run_cost, b = p.seg_prefix[seg + 1];
   const int64_t N = p.seg_prefix[p.num_segments];
   const int64_t W = min((int64_t)p.num_waves, N);
   int n = 0;

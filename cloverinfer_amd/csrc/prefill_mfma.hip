@@ -67,15 +67,20 @@ __device__ __forceinline__ u32x4 vt_read(const uint16_t *lo, const uint16_t *hi)
   return (u32x4){ua[0], ua[1], ub[0], ub[1]};
 }
 
-// Two bf16 values (one 32-bit word) as two fp16 values; records the largest
-// magnitude seen in `amax`.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, float &amax) {
+// Two bf16 values (one 32-bit word) as two fp16 values. `hmax` collects the
+// largest fp16 magnitude bits of each half (packed unsigned 16-bit maxima):
+// a half at or above 0x7c00 is an fp16 infinity or NaN, i.e. a bf16 value
+// that did not fit (magnitude >= 65520 rounds to infinity) or a NaN.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, uint32_t &hmax) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   const float a = __builtin_bit_cast(float, w << 16);
   const float b = __builtin_bit_cast(float, w & 0xffff0000u);
-  amax = fmaxf(amax, fmaxf(fabsf(a), fabsf(b)));
-  const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)a);
-  const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)b);
-  return lo | (hi << 16);
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+  hmax = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, hmax),
+                                                                __builtin_bit_cast(u16x2, h & 0x7fff7fffu)));
+  return h;
 }
 
 template <typename T, int D>
@@ -174,38 +179,50 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
                            ? base_pos + q0 + wave_row0 / G : -1;
 
   // Tile loader: thread handles chunk (tid % CPR) of rows tid / CPR + RPP*i.
+  // One load instruction of a wave covers WROWS consecutive rows, which lie
+  // in one block (the launcher requires block_size >= WROWS): the block id is
+  // read with a scalar load through the constant address space (the kernel
+  // never writes the table) and the row address is a scalar base plus a
+  // per-lane constant 32-bit offset.
+  constexpr int WROWS = 64 / CPR;
   const int lchunk = tid % CPR;
   const int lrow = tid / CPR;
+  const int wrow = WROWS * wave;  // first row of the wave's load instructions
+  // Byte strides as 32-bit values (the launcher checks that a block's rows
+  // fit in 2^32 bytes).
+  const uint32_t sblk32 = (uint32_t)kv.sblk, stok32 = (uint32_t)kv.stok;
+  const uint32_t bmask = (1u << kv.block_shift) - 1u;
+  const uint32_t lane_off = (uint32_t)(lrow - wrow) * stok32 + (uint32_t)lchunk * 16u;
+  typedef const int32_t __attribute__((address_space(4))) *cint_t;
+  const cint_t brow = (cint_t)kv.bt;
   u32x4 kreg[PASSES], vreg[PASSES];
   bool rvalid[PASSES];  // the loaded rows are readable tokens
-  int rblk[PASSES];     // block of each row of the tile to load next (-1: none)
-  // Block-table entries are fetched one tile before their rows are loaded and
-  // only turned into addresses then: a use right after the fetch would wait
-  // for every vector load in flight (the counter is in order).
+  int rblk[PASSES];     // block of the wave's rows of the tile to load next (-1: none)
+  // Block-table entries are fetched one tile before their rows are loaded.
   auto fetch_blocks = [&](int tile) {
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
-      const int t = tile * kBK + lrow + RPP * i;
-      rblk[i] = (tile < ntiles && t < kv_end) ? kv.bt[t >> kv.block_shift] : -1;
+      const int t0 = tile * kBK + wrow + RPP * i;
+      rblk[i] = (tile < ntiles && t0 < kv_end) ? brow[t0 >> kv.block_shift] : -1;
     }
   };
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
-      const int t = tile * kBK + lrow + RPP * i;
-      const bool ok = (unsigned)rblk[i] < kv.num_blocks;
-      const int64_t off = ok ? rblk[i] * kv.sblk + (t & ((1 << kv.block_shift) - 1)) * kv.stok : 0;
+      const uint32_t t0 = (uint32_t)(tile * kBK + wrow + RPP * i);
+      const bool ok = (unsigned)rblk[i] < kv.num_blocks && (int)t0 + (lrow - wrow) < kv_end;
+      const uint64_t wb = (uint64_t)(uint32_t)rblk[i] * sblk32 + (t0 & bmask) * stok32;
       const u32x4 z = {0u, 0u, 0u, 0u};
       rvalid[i] = ok;
-      kreg[i] = ok ? load_vec<u32x4>(kv.kbase + off + lchunk * 16) : z;
-      vreg[i] = ok ? load_vec<u32x4>(kv.vbase + off + lchunk * 16) : z;
+      kreg[i] = ok ? load_vec<u32x4>(kv.kbase + wb + lane_off) : z;
+      vreg[i] = ok ? load_vec<u32x4>(kv.vbase + wb + lane_off) : z;
     }
   };
   // Stage the loaded rows into LDS buffer buf. The fast pass stores V as
   // fp16 and flags values that do not fit; the exact pass stores V as is.
   auto store_tile = [&](int buf, auto exact_c) {
     constexpr bool EXACT = decltype(exact_c)::value;
-    float amax = 0.f;
+    uint32_t hmax = 0u;
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int row = lrow + RPP * i;
@@ -213,18 +230,18 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       u32x4 v = vreg[i];
       if constexpr (kBf16 && !EXACT) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e], amax);
+        for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e], hmax);
       }
       store_vec<u32x4>(&sV[buf][row * VROW + lchunk * 8], v);
       if (lchunk == 0) sValid[buf][row] = rvalid[i] ? 1 : 0;
     }
-    // 65504 is the largest finite fp16; bf16 has nothing between it and 2^16.
-    // NaN compares false here and converts to a NaN, as it should.
-    if (kBf16 && !EXACT && !(amax <= 65504.f)) sOvf = 1;
+    if (kBf16 && !EXACT && ((hmax & 0xffffu) >= 0x7c00u || (hmax >> 16) >= 0x7c00u)) sOvf = 1;
   };
 
   f32x4 o[kRT][CH];
   float m_run[kRT];
+  float thr[kRT];   // rescale threshold per row (see softmax)
+  float msub[kRT];  // m_run * c (0 while m_run is -inf)
   // Row sums of P, accumulated by MFMA against an all-ones B operand (so in
   // the C layout of o: element e is row 4j + e), consistent with the
   // rounded P that P.V uses.
@@ -248,6 +265,8 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
 #pragma unroll
       for (int m = 0; m < CH; ++m) o[rt][m] = (f32x4){0.f, 0.f, 0.f, 0.f};
       m_run[rt] = kNegInf;
+      thr[rt] = kNegInf;
+      msub[rt] = 0.f;
       lsum[rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
     f32x4 sacc[2][kRT];     // scores of the step between M and V
@@ -323,7 +342,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
         }
       }
     };
-    // Online softmax of step g.
+    // Online softmax of step g. The running max is raised only when some
+    // score exceeds it by more than 2^8 (log2 units), or it is still -inf.
+    // Each lane tests its own eight scores of the row against the threshold
+    // thr = m_run + 8 / c; the row maximum over the four lanes that hold the
+    // row is only formed when some lane of the wave passes it.
     auto softmax = [&](int g, bool full) {
       if (!full) mask_step(g);
       float pf[kRT][8];
@@ -334,16 +357,17 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mx = fmaxf(mx, sacc[h][rt][e]);
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        // Raise the running max only when the scores exceed it by > 2^8 (or
-        // it is still -inf).
-        const bool grow = (mx - m_run[rt]) * c > kRescaleLog2;
-        if (__any(grow)) {
+        if (__any(mx > thr[rt])) {
+          mx = fmaxf(mx, shfl_xor(mx, 16));
+          mx = fmaxf(mx, shfl_xor(mx, 32));
           const float m_new = fmaxf(m_run[rt], mx);
           // 0 when the row had no visible token yet, 1 if its max is unchanged.
           const float alpha = m_new == kNegInf ? 1.f : fast_exp2((m_run[rt] - m_new) * c);
           m_run[rt] = m_new;
+          // m_new + 8 / c is +inf when c is tiny (a zero scale): P is then 1
+          // for every visible token and no rescale is ever needed again.
+          thr[rt] = m_new == kNegInf ? kNegInf : m_new + kRescaleLog2 / c;
+          msub[rt] = m_new == kNegInf ? 0.f : m_new * c;
           // Row 4j + e of o[rt][m] and lsum[rt] is element e.
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -353,12 +377,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
             for (int m = 0; m < CH; ++m) o[rt][m][e] *= a;
           }
         }
-        const float msub = m_run[rt] == kNegInf ? 0.f : m_run[rt] * c;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            pf[rt][4 * h + e] = fast_exp2(__builtin_fmaf(sacc[h][rt][e], c, -msub));
+            pf[rt][4 * h + e] = fast_exp2(__builtin_fmaf(sacc[h][rt][e], c, -msub[rt]));
       }
       // P's k-slot 4h + e is token 32(g%2) + 16h + 4j + e, as in pv().
 #pragma unroll
@@ -400,12 +423,19 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       }
       const bool full = tile_full(tile);
       const int g = 2 * tile;
+      // The MFMA phases run at raised wave priority: the SIMD's arbiter then
+      // issues the next MFMA as soon as the matrix core takes it, and the
+      // other wave's softmax fills the issue slots in between.
       if (lag && tile > 0) softmax_step(g - 1, full_prev);
+      __builtin_amdgcn_s_setprio(1);
       qk(g);
       if (tile > 0) pv(g - 1);
+      __builtin_amdgcn_s_setprio(0);
       softmax_step(g, full);
+      __builtin_amdgcn_s_setprio(1);
       qk(g + 1);
       pv(g);
+      __builtin_amdgcn_s_setprio(0);
       if (!lag) softmax_step(g + 1, full);
       full_prev = full;
 
@@ -464,12 +494,18 @@ hipError_t launch_t(const PrefillParams &p, hipStream_t stream) {
 }  // namespace
 
 bool prefill_mfma_supported(DType dt, int head_dim, int block_size) {
-  (void)block_size;
-  return (dt == DType::F16 || dt == DType::BF16) && (head_dim == 64 || head_dim == 128);
+  // A wave's load instruction covers 512 / head_dim rows of one block.
+  return (dt == DType::F16 || dt == DType::BF16) && (head_dim == 64 || head_dim == 128) &&
+         block_size >= 512 / head_dim;
 }
 
 hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream) {
-  if (p.group > kRows) return launch_prefill_valu(p, dt, stream);
+  // The tile loader computes addresses inside a block with 32-bit byte
+  // offsets; pools with larger blocks take the VALU kernel.
+  const uint64_t eb = 2, lim = (uint64_t)1 << 32;
+  const bool narrow = (uint64_t)p.kv_stride_block * eb < lim &&
+                      ((uint64_t)p.kv_stride_token * eb << p.block_shift) < lim;
+  if (p.group > kRows || !narrow) return launch_prefill_valu(p, dt, stream);
   if (dt == DType::BF16) return launch_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_t<_Float16>(p, stream);
   return hipErrorInvalidValue;

@@ -42,17 +42,47 @@ class _Request:
         self.row = row  # row of the device block table
 
 
+# Names accepted for the pool dtype: the resident KV dtype strings of the
+# reference's PIM backends (src/core/attention_backend.py:201, "fp32" and
+# "fp16"; src/core/config.py:38) plus bf16, and torch's own names.
+_KV_DTYPES = {
+    "fp32": torch.float32, "float32": torch.float32,
+    "fp16": torch.float16, "float16": torch.float16, "half": torch.float16,
+    "bf16": torch.bfloat16, "bfloat16": torch.bfloat16,
+}
+
+
+def _kv_dtype(value) -> Optional[torch.dtype]:
+    if value is None or isinstance(value, torch.dtype):
+        if value is not None and value not in _KV_DTYPES.values():
+            raise ValueError(f"Unsupported kv dtype: {value}")
+        return value
+    name = str(value).lower().replace("torch.", "")
+    if name not in _KV_DTYPES:
+        raise ValueError(f"Unsupported resident_kv_dtype: {value}")
+    return _KV_DTYPES[name]
+
+
 class GpuAttentionBackend:
     def __init__(self, num_blocks: int = 4096, block_size: int = 16, device: str = "cuda",
-                 kv_dtype: Optional[torch.dtype] = None, partition_size: Optional[int] = None):
+                 kv_dtype=None, partition_size: Optional[int] = None,
+                 resident_kv_dtype=None):
+        """``kv_dtype`` (or ``resident_kv_dtype``, the reference's knob name
+        as the scheduler passes it to KV-resident backends) selects the pool
+        dtype: a torch dtype or "fp32" / "fp16" / "bf16". Default: the dtype of
+        the first request's KV. Queries, keys and values are converted to it;
+        outputs come back in each query's dtype."""
         if num_blocks <= 0 or block_size <= 0 or block_size & (block_size - 1):
             raise ValueError("num_blocks must be positive and block_size a power of two")
+        if kv_dtype is not None and resident_kv_dtype is not None and \
+                _kv_dtype(kv_dtype) != _kv_dtype(resident_kv_dtype):
+            raise ValueError("kv_dtype and resident_kv_dtype disagree")
         self.num_blocks = num_blocks
         self.block_size = block_size
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("GpuAttentionBackend needs a HIP device (there is no CPU fallback)")
-        self.kv_dtype = kv_dtype
+        self.kv_dtype = _kv_dtype(kv_dtype if kv_dtype is not None else resident_kv_dtype)
         self.partition_size = partition_size
         self.k_pools: Optional[torch.Tensor] = None  # [L, NB, bs, Hkv, D]
         self.v_pools: Optional[torch.Tensor] = None
@@ -293,12 +323,18 @@ class GpuAttentionBackend:
             self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
         slots_dev = wide_dev[:n]
         ctx_dev = meta_dev[2 * (n + 3 * nu):2 * (n + 3 * nu) + n]
-        kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots_dev)
         bt = self.tables.rows(rows, meta_dev[2 * (n + 3 * nu) + n:])
         ctx_out = torch.empty_like(q)
-        kernels.paged_attention(ctx_out, q, self.k_pools[layer], self.v_pools[layer], bt,
-                                ctx_dev, bs, max(lens), scale=score_scale,
-                                partition_size=self.partition_size)
+        kp, vp = self.k_pools[layer], self.v_pools[layer]
+        if self.partition_size is None and kernels.append_fusable(q, kp, n):
+            # Append and decode in one call: the new rows land at position
+            # lens - 1, the slots computed above.
+            kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens), k, v,
+                                           scale=score_scale)
+        else:
+            kernels.reshape_and_cache(k, v, kp, vp, slots_dev)
+            kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens),
+                                    scale=score_scale, partition_size=self.partition_size)
         if layer == self.num_layers - 1:
             for req in reqs:
                 req.context_len += 1

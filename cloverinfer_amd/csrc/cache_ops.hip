@@ -68,7 +68,53 @@ __global__ void __launch_bounds__(kThreads) reshape_and_cache_elem(const CachePa
 
 bool aligned16(const void *ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Append of one decode step, the slot taken from the block table: sequence
+// s's new rows key_new/value_new[s] go to its context position
+// context_lens[s] - 1 when 1 <= context_lens[s] <= min(max_context_len,
+// max_blocks_per_seq * block_size) and that position's block-table entry is
+// in [0, num_blocks). One thread per 16-byte chunk of one (sequence, head)
+// row of both the key and the value.
+__global__ void __launch_bounds__(kThreads)
+append_by_table_vec16(const DecodeParams p, int chunks_per_row, int elem_bytes) {
+  // The launcher guarantees num_seqs*num_kv_heads*chunks_per_row < 2^31.
+  const uint32_t gid = blockIdx.x * kThreads + threadIdx.x;
+  const uint32_t rows = (uint32_t)p.num_seqs * (uint32_t)p.num_kv_heads;
+  const uint32_t row = gid / (uint32_t)chunks_per_row;
+  if (row >= rows) return;
+  const int chunk = (int)(gid - row * (uint32_t)chunks_per_row);
+  const int s = (int)(row / (uint32_t)p.num_kv_heads);
+  const int head = (int)(row - (uint32_t)s * (uint32_t)p.num_kv_heads);
+  const int len = p.context_lens[s];
+  const int cap = min(p.max_context_len, p.max_blocks_per_seq << p.block_shift);
+  if (len < 1 || len > cap) return;
+  const int pos = len - 1;
+  const int blk = p.block_tables[(int64_t)s * p.max_blocks_per_seq + (pos >> p.block_shift)];
+  if ((unsigned)blk >= (unsigned)p.num_blocks) return;
+  const int64_t eb = elem_bytes;
+  const int64_t dst = ((int64_t)blk * p.kv_stride_block +
+                       (int64_t)(pos & ((1 << p.block_shift) - 1)) * p.kv_stride_token +
+                       (int64_t)head * p.kv_stride_head) * eb + chunk * 16;
+  const int64_t src = ((int64_t)s * p.new_stride_seq + (int64_t)head * p.new_stride_head) * eb +
+                      chunk * 16;
+  const u32x4 kv = load_vec<u32x4>((const char *)p.key_new + src);
+  const u32x4 vv = load_vec<u32x4>((const char *)p.value_new + src);
+  store_vec<u32x4>((char *)const_cast<void *>(p.k_cache) + dst, kv);
+  store_vec<u32x4>((char *)const_cast<void *>(p.v_cache) + dst, vv);
+}
+
 }  // namespace
+
+hipError_t launch_append_by_table(const DecodeParams &p, hipStream_t stream) {
+  // Validated by the caller: 16-byte aligned pointers and strides, 16-bit
+  // elements, rows of head_dim * 2 bytes.
+  const int chunks = p.head_dim * 2 / 16;
+  const int64_t work = (int64_t)p.num_seqs * p.num_kv_heads * chunks;
+  if (work == 0) return hipSuccess;
+  if (work >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  const unsigned blocks = (unsigned)((work + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(append_by_table_vec16, dim3(blocks), dim3(kThreads), 0, stream, p, chunks, 2);
+  return hipGetLastError();
+}
 
 hipError_t launch_reshape_and_cache(const CacheParams &p, hipStream_t stream) {
   if (p.num_tokens == 0 || p.num_kv_heads == 0) return hipSuccess;

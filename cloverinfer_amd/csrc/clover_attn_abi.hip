@@ -350,6 +350,30 @@ int clv_paged_decode_balanced(const clv_decode_args *a, int32_t num_waves, void 
   return clv_balanced_reduce(a, num_waves, workspace, workspace_bytes, stream);
 }
 
+int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const void *value_new,
+                            int64_t new_stride_seq, int64_t new_stride_head, int32_t num_waves,
+                            void *workspace, size_t workspace_bytes, clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_balanced(a, num_waves, workspace, workspace_bytes, &p);
+  if (st != CLV_OK || p.num_seqs == 0) return st;
+  const int eb = elem_bytes(a->dtype);
+  if (!key_new || !value_new || !aligned16(key_new) || !aligned16(value_new) ||
+      !stride16(new_stride_seq, eb) || !stride16(new_stride_head, eb))
+    return CLV_EINVAL;
+  p.key_new = key_new;
+  p.value_new = value_new;
+  p.new_stride_seq = new_stride_seq;
+  p.new_stride_head = new_stride_head;
+  const hipStream_t s = (hipStream_t)stream;
+  if (clv::stream_appends_in_kernel(a->head_dim, a->block_size, p.group)) {
+    p.append_new = 1;
+  } else if (clv::launch_append_by_table(p, s) != hipSuccess) {
+    return CLV_ELAUNCH;
+  }
+  if (clv::launch_decode_stream(p, (DType)a->dtype, s) != hipSuccess) return CLV_ELAUNCH;
+  return clv::launch_stream_reduce(p, (DType)a->dtype, s) == hipSuccess ? CLV_OK : CLV_ELAUNCH;
+}
+
 int clv_chunked_prefill(const clv_prefill_args *a, clv_stream_t stream) {
   if (a == nullptr) return CLV_EINVAL;
   if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;

@@ -40,6 +40,14 @@ struct DecodeParams {
   int32_t num_segments;   // num_seqs * num_kv_heads * n_gchunks
   int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
   int32_t *slot_prefix;   // [num_segments + 1] exclusive prefix of partials per segment
+  // Fused append (balanced mode): when append_new is set, sequence s's new
+  // key/value rows key_new/value_new[s] ([num_kv_heads, head_dim], strides in
+  // elements) are written at its context position context_lens[s] - 1 by the
+  // wave that computes that position, before it loads it.
+  int32_t append_new;
+  const void *key_new;
+  const void *value_new;
+  int64_t new_stride_seq, new_stride_head;
 };
 
 // Largest segment count the balanced mode keeps in LDS.
@@ -85,11 +93,18 @@ hipError_t launch_splitk_reduce(const DecodeParams &p, DType dt, hipStream_t str
 hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_stream_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream);
+// Writes key_new/value_new[s] at position context_lens[s] - 1 of every
+// sequence (slot from its block table), for the decode shapes whose stream
+// kernel does not append itself.
+hipError_t launch_append_by_table(const DecodeParams &p, hipStream_t stream);
 hipError_t launch_prefill_valu(const PrefillParams &p, DType dt, hipStream_t stream);
 
 // Whether the MFMA decode kernel covers this shape/dtype.
 bool decode_mfma_supported(DType dt, int head_dim, int block_size);
 bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments);
+// Whether the stream kernel writes the appended token itself (fused append)
+// for this shape; otherwise launch_append_by_table runs first.
+bool stream_appends_in_kernel(int head_dim, int block_size, int group);
 bool prefill_mfma_supported(DType dt, int head_dim, int block_size);
 
 }  // namespace clv

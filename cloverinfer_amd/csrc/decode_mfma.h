@@ -61,6 +61,24 @@ __device__ __forceinline__ SegGeom seg_geom(const DecodeParams &p, int s, int kv
   return g;
 }
 
+// One token's key/value rows (16-bit elements, head_dim 128, at knew / vnew)
+// written at byte offset `row_off` of the pools at kbase / vbase, by the
+// lanes that load them back in the K-transpose path of DecodeWave: a row r
+// of a step is loaded by the lanes with j = r / 4, each its 16-byte chunk
+// n16. A load in the same wave that follows the store therefore sees the new
+// values without any cross-lane ordering.
+__device__ __forceinline__ void kt_store_row(const char *kbase, const char *vbase, int64_t row_off,
+                                             int r, const uint16_t *knew, const uint16_t *vnew) {
+  const int lane = threadIdx.x & 63;
+  if ((lane >> 4) == (r & 15) >> 2) {
+    const int64_t off = row_off + (lane & 15) * 16;
+    const u32x4 kv = load_vec<u32x4>(knew + (lane & 15) * 8);
+    const u32x4 vv = load_vec<u32x4>(vnew + (lane & 15) * 8);
+    store_vec<u32x4>(const_cast<char *>(kbase) + off, kv);
+    store_vec<u32x4>(const_cast<char *>(vbase) + off, vv);
+  }
+}
+
 // UNI: block_size >= 16, so a step sits in one block and its block-table
 // entry is wave-uniform (scalar load, buffer loads). Otherwise (block_size 4
 // or 8) lanes look up their own rows.

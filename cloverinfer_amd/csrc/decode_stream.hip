@@ -72,7 +72,8 @@ __device__ int block_exclusive_scan(int *buf, int n, int *tmp) {
   return total;
 }
 
-template <typename T, int D, bool UNI, int DEPTH>
+// APPEND (K-transpose path only): fused append, see below.
+template <typename T, int D, bool UNI, int DEPTH, bool APPEND = false>
 __global__ void __launch_bounds__(kThreads)
 paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
                     const int32_t *__restrict__ lens, float *__restrict__ ws_o,
@@ -138,6 +139,34 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   w.init(p);
   w.set_k_lds(s_kt[uni(threadIdx.x >> 6)]);
 
+  if constexpr (APPEND) {
+    // Fused append: the wave that holds a segment's last step writes the
+    // sequence's new token (position ctx - 1) before its run loop. Only that
+    // wave ever loads the row (one query-head chunk per kv head on this
+    // path), with the lanes that wrote it (kt_store_row).
+    static_assert(UNI && D == 128, "the fused append mirrors the K-transpose loads");
+    for (int sg = seg; sg < nseg && uni(s_seg[sg + 1]) - 1 < en; ++sg) {
+      const int lst = uni(s_seg[sg + 1]) - 1;
+      if (lst < st || lst < uni(s_seg[sg]) + K) continue;  // not ours, or no real steps
+      const int s_ = sg / per_seq;
+      const int kvh = sg - s_ * per_seq;  // one query-head chunk per kv head
+      const int ctx = clamp_ctx(p, lens, s_);
+      if (ctx != scalar_load_i32(lens + s_)) continue;  // the new position is not attended
+      const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
+      const int pos = ctx - 1;
+      const int blk = scalar_load_i32(geo.bt + (pos >> p.block_shift));
+      if ((unsigned)blk >= (unsigned)p.num_blocks) continue;
+      const int64_t row_off =
+          ((int64_t)blk * p.kv_stride_block + (int64_t)(pos & ((1 << p.block_shift) - 1)) *
+                                                  p.kv_stride_token) * (int64_t)sizeof(T);
+      const int64_t src = (int64_t)s_ * p.new_stride_seq + (int64_t)kvh * p.new_stride_head;
+      kt_store_row(geo.kbase, geo.vbase, row_off, pos,
+                   (const uint16_t *)p.key_new + src, (const uint16_t *)p.value_new + src);
+    }
+    __builtin_amdgcn_s_waitcnt(0);      // the stores are done before any load is issued
+    __asm__ volatile("" ::: "memory");  // and the compiler keeps them ahead of the loads
+  }
+
   // The span is cut at segment borders into runs. Each run loads its Q rows,
   // keeps DEPTH steps of loads in flight (a ring of register sets refilled
   // right after each step is folded) and ends with one partial.
@@ -158,6 +187,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     const int ng = min(16, p.group - g0);
     const int ctx = clamp_ctx(p, lens, s_);
     const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
+
     // Q loads go out first and are waited for only after the ring below is
     // issued, so a run start costs one memory latency, not two.
     u32x4 qraw[WV::NQK];
@@ -234,6 +264,15 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
 template <typename T, int D, int DEPTH>
 hipError_t launch_stream_tdd(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((p.num_waves + kWaves - 1) / kWaves));
+  if constexpr (D == 128) {
+    if (p.append_new) {  // set only where stream_appends_in_kernel holds
+      if (p.block_shift < 4) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, true>), grid, dim3(kThreads), 0,
+                         stream, p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l,
+                         p.seg_prefix, p.slot_prefix);
+      return hipGetLastError();
+    }
+  }
   if (p.block_shift >= 4)
     hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH>), grid, dim3(kThreads), 0, stream,
                        p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix,
@@ -279,6 +318,12 @@ hipError_t launch_sreduce_t(const DecodeParams &p, hipStream_t stream) {
 
 bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments) {
   return decode_mfma_supported(dt, head_dim, block_size) && num_segments <= kStreamMaxSegments;
+}
+
+bool stream_appends_in_kernel(int head_dim, int block_size, int group) {
+  // The K-transpose path (a 16-token step inside one block, head_dim 128)
+  // with one query-head chunk per kv head.
+  return head_dim == 128 && block_size >= 16 && group <= 16;
 }
 
 hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream) {

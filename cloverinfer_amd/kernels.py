@@ -211,6 +211,50 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     )
 
 
+def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, block_tables: torch.Tensor,
+                           context_lens: torch.Tensor, block_size: int, max_context_len: int,
+                           key_new: torch.Tensor, value_new: torch.Tensor,
+                           scale: float | None = None, num_waves: int = 0) -> None:
+    """One decode step of the append-then-attend protocol in one call
+    (clv_paged_decode_append): sequence s's ``key_new[s]``/``value_new[s]``
+    ([num_kv_heads, head_dim]) are written at its position
+    ``context_lens[s] - 1`` (slot from its block-table row), then ``out`` =
+    :func:`paged_attention` over all ``context_lens[s]`` tokens. Equal to
+    :func:`reshape_and_cache` with those slots followed by
+    :func:`paged_attention`; covers the shapes of the balanced decode
+    (:func:`append_fusable`), raises otherwise."""
+    dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens, key_new, value_new)
+    a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                     max_context_len, scale)
+    if not balanced_supported(a):
+        raise NotImplementedError("paged_attention_append covers the balanced decode's shapes only")
+    shape = (a.num_seqs, a.num_kv_heads, a.head_dim)
+    if key_new.shape != shape or value_new.shape != shape:
+        raise ValueError(f"key_new/value_new must be {shape}, got {tuple(key_new.shape)} and "
+                         f"{tuple(value_new.shape)}")
+    if key_new.dtype != k_cache.dtype or value_new.dtype != k_cache.dtype:
+        raise ValueError("key_new/value_new dtype must match the cache dtype")
+    if key_new.stride() != value_new.stride() or key_new.stride(2) != 1:
+        key_new, value_new = key_new.contiguous(), value_new.contiguous()
+    lib = _native.load()
+    nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
+                                              a.head_dim, num_waves)
+    ws = splitk_workspace(dev, nbytes)
+    _native.check(lib.clv_paged_decode_append(a, key_new.data_ptr(), value_new.data_ptr(),
+                                              key_new.stride(0), key_new.stride(1), num_waves,
+                                              ws.data_ptr(), ws.numel(), _stream(dev)),
+                  "clv_paged_decode_append")
+
+
+def append_fusable(q: torch.Tensor, k_cache: torch.Tensor, num_seqs: int) -> bool:
+    """Whether :func:`paged_attention_append` covers this decode shape."""
+    hq, hkv, d = q.shape[1], k_cache.shape[2], k_cache.shape[3]
+    nseg = num_seqs * hkv * ((hq // hkv + 15) // 16)
+    return (k_cache.dtype in (torch.float16, torch.bfloat16) and d in (64, 128)
+            and k_cache.shape[1] >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
+
+
 def workspace_bytes(a: _native.DecodeArgs, partition_size: int) -> int:
     return _native.load().clv_splitk_workspace_bytes(a.num_seqs, a.num_heads, a.head_dim,
                                                      a.max_context_len, partition_size)

@@ -203,6 +203,31 @@ int clv_balanced_reduce(const clv_decode_args *args, int32_t num_waves,
                         const void *workspace, size_t workspace_bytes,
                         clv_stream_t stream);
 
+/*
+ * One decode step of the reference's append-then-attend protocol
+ * (CpuAttentionBackend.decode_layer, src/core/attention_backend.py:105-118;
+ * KVCacheManager.write_new_kv then .attention,
+ * src/core/memory_manager.py:123-190) in one call: sequence s's new key and
+ * value rows key_new[s], value_new[s] ([num_kv_heads, head_dim], strides in
+ * elements) are written at its context position context_lens[s] - 1 (the
+ * slot its block table names), and its query rows attend to all
+ * context_lens[s] tokens, the new one included. Same result as
+ * clv_reshape_and_cache with those slots followed by
+ * clv_paged_decode_balanced, and the same shapes and workspace as the latter
+ * (CLV_EUNSUPPORTED otherwise). For head_dim 128, block_size >= 16 and at
+ * most 16 query heads per kv head, the decode kernel writes the rows itself
+ * (no separate append launch). A sequence appends nothing when
+ * context_lens[s] is outside [1, min(max_context_len,
+ * max_blocks_per_seq*block_size)] or the slot's block-table entry is outside
+ * [0, num_blocks). k_cache and v_cache are written. No counterpart kernel
+ * exists in the reference.
+ */
+int clv_paged_decode_append(const clv_decode_args *args, const void *key_new,
+                            const void *value_new, int64_t new_stride_seq,
+                            int64_t new_stride_head, int32_t num_waves,
+                            void *workspace, size_t workspace_bytes,
+                            clv_stream_t stream);
+
 /* Workspace bytes of clv_paged_decode_balanced (num_waves <= 0: default). */
 size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads,
                                     int32_t num_kv_heads, int32_t head_dim,

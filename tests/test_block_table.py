@@ -62,3 +62,4 @@ def test_uploaded_updates_match_queued_ones():
     assert t.take_pending() == []
     t.apply(torch.tensor(upd, dtype=torch.int64).t().contiguous(), max(c for _, c, _ in upd))
     assert t.rows([a, b]).tolist() == [[1, 2, 9, -1], [3, 4, 5, -1]]
+

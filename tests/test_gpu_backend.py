@@ -163,3 +163,31 @@ def test_init_from_hf_cache_matches_normalised_ingest(layout):
         assert_attention_close(a.decode_layer_batch(it)[0], cpu.decode_layer_batch(it)[0],
                                what=f"layer {layer}")
     assert a.get_context_len("r") == cpu.get_context_len("r") == T + 1
+
+
+@pytest.mark.parametrize("knob", [{"resident_kv_dtype": "fp16"}, {"kv_dtype": "bf16"}])
+def test_resident_kv_dtype_knob(knob):
+    """fp32 payloads with the pools in fp16 / bf16 (the reference's
+    resident_kv_dtype knob): outputs in fp32, equal to the restated
+    CpuAttentionBackend fed the same values rounded to the pool dtype (the
+    backend converts q, k and v to the pool dtype)."""
+    g = torch.Generator().manual_seed(51)
+    pool_dt = torch.float16 if "resident_kv_dtype" in knob else torch.bfloat16
+    rnd = lambda t: t.to(pool_dt).float()
+    hq, hkv, d, layers = 8, 2, 64, 2
+    gpu = create_attention_backend("gpu", {"num_blocks": 64, "block_size": 16, **knob})
+    cpu = CpuAttentionOracle()
+    kv = [{"key": torch.randn(37, hkv, d, generator=g), "value": torch.randn(37, hkv, d, generator=g)}
+          for _ in range(layers)]
+    assert gpu.init_request("r", kv) == 37
+    cpu.init_request("r", [{"key": rnd(x["key"]), "value": rnd(x["value"])} for x in kv])
+    assert gpu.get_debug_info()["kv_dtype"] == str(pool_dt)
+    for layer in range(layers):
+        it = {"request_id": "r", "layer_idx": layer, "query": torch.randn(1, hq, d, generator=g),
+              "key": torch.randn(1, hkv, d, generator=g), "value": torch.randn(1, hkv, d, generator=g),
+              "score_scale": 0.125}
+        got = gpu.decode_layer_batch([it])[0]
+        ref = cpu.decode_layer_batch([{**it, "query": rnd(it["query"]), "key": rnd(it["key"]),
+                                       "value": rnd(it["value"])}])[0]
+        assert got.dtype == torch.float32
+        assert_attention_close(got, ref, what=f"layer {layer}")

@@ -293,6 +293,79 @@ def bench_decode(args, cfg):
     return result
 
 
+def bench_decode_fp8(args):
+    """The GQA Qwen2.5-7B decode batch with fp8 (OCP e4m3) pools: K/V are
+    the same seeded N(0,1) data stored as e4m3 with scale 1 per kv head; q
+    and out stay bf16. A step is one clv_paged_decode_fp8 call (stream decode
+    + merge)."""
+    import torch
+    from cloverinfer_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    cfg = DECODE_CONFIGS["qwen7b"]
+    log("building workload qwen7b_fp8")
+    w = decode_workload(cfg, dev)
+    k8 = w["k"].float().clamp(-448, 448).to(kernels.FP8)
+    v8 = w["v"].float().clamp(-448, 448).to(kernels.FP8)
+    del w["k"], w["v"]
+    ones = torch.ones(cfg["hkv"], dtype=torch.float32, device=dev)
+    out = torch.empty_like(w["q"])
+    max_ctx = max(w["ctx"])
+    a = kernels.decode_args(out, w["q"], k8, v8, w["table"], w["ctx_dev"], w["bs"], max_ctx,
+                            scale=w["scale"])
+    lib = kernels._native.load()
+    stream = torch.cuda.current_stream(dev)
+    waves = args.waves or lib.clv_default_num_waves_fp8()
+    ws = kernels.splitk_workspace(dev, kernels.balanced_workspace_bytes(a, waves))
+
+    def step():
+        kernels._native.check(lib.clv_paged_decode_fp8(a, ones.data_ptr(), ones.data_ptr(),
+                                                       waves, ws.data_ptr(), ws.numel(),
+                                                       stream.cuda_stream), "clv_paged_decode_fp8")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    torch.cuda._sleep(50_000_000)
+    for e in ev:
+        e[0].record(stream)
+        step()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    call_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
+    ctx = w["ctx"]
+    kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * 1 * 2
+    qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * 2 * 2
+    tbl_bytes = sum(math.ceil(c / w["bs"]) for c in ctx) * 4 + len(ctx) * 4
+    algo = kv_bytes + qo_bytes + tbl_bytes
+    log(f"step {ms:.4f} ms, decode + merge {call_us:.1f} us")
+    return {
+        "metric": "decode-attn HBM GB/s, fp8 KV pools, GQA-7B shape, 1 GPU",
+        "value": algo / (ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8-kv/bf16",
+        "data": "synthetic N(0,1) q/K/V, random init, seeded; K/V stored as e4m3, scale 1",
+        "config": {"workload": "paged decode over fp8 (e4m3) pools, GQA Qwen2.5-7B shape: 128 seqs, "
+                               "28 q / 4 kv heads, head_dim 128, block 16, q/out bf16, "
+                               "context U[256,8192] seeded per sequence",
+                   "total_context_tokens": sum(ctx), "algorithmic_bytes_per_step": algo,
+                   "seed": cfg["seed"]},
+        "tokens_per_s": len(ctx) / (ms * 1e-3),
+        "kernels_us": {"paged_decode_fp8_with_merge": call_us},
+        "roofline": {"bound": "hbm", "kernel": "paged_decode_stream (fp8) + merge",
+                     "achieved": algo / (call_us * 1e-6) / 1e9, "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": algo / (call_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                     "traffic": None},
+    }
+
+
 def bench_prefill(args):
     """Chunked prefill, 8 sequences x (4096 cached + 512 new), 32 q / 8 kv
     heads, head_dim 128, bf16: a step appends the 512 new K/V rows of every
@@ -443,7 +516,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen7b",
-                    choices=sorted(DECODE_CONFIGS) + ["prefill", "copy", "node"])
+                    choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass, -1 or default: automatic)")
     ap.add_argument("--waves", type=int, default=0,
@@ -462,7 +535,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
-    if args.config == "prefill":
+    if args.config == "qwen7b_fp8":
+        result = bench_decode_fp8(args)
+    elif args.config == "prefill":
         result = bench_prefill(args)
     elif args.config == "copy":
         result = bench_copy(args)

@@ -151,8 +151,16 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, ctypes.c_int64, ctypes.c_int64, _c_i32,
          _c_ptr, ctypes.c_size_t, _c_ptr],
     ),
+    "clv_reshape_and_cache_fp8": (
+        ctypes.c_int, [ctypes.POINTER(CacheArgs), _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "clv_paged_decode_fp8": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
     "clv_balanced_workspace_bytes": (ctypes.c_size_t, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "clv_default_num_waves": (_c_i32, []),
+    "clv_default_num_waves_fp8": (_c_i32, []),
     "clv_chunked_prefill": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), _c_ptr]),
 }
 

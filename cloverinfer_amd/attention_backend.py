@@ -49,6 +49,8 @@ _KV_DTYPES = {
     "fp32": torch.float32, "float32": torch.float32,
     "fp16": torch.float16, "float16": torch.float16, "half": torch.float16,
     "bf16": torch.bfloat16, "bfloat16": torch.bfloat16,
+    "fp8": torch.float8_e4m3fn, "fp8_e4m3": torch.float8_e4m3fn,
+    "float8_e4m3fn": torch.float8_e4m3fn,
 }
 
 
@@ -66,12 +68,15 @@ def _kv_dtype(value) -> Optional[torch.dtype]:
 class GpuAttentionBackend:
     def __init__(self, num_blocks: int = 4096, block_size: int = 16, device: str = "cuda",
                  kv_dtype=None, partition_size: Optional[int] = None,
-                 resident_kv_dtype=None):
+                 resident_kv_dtype=None, kv_scale=1.0):
         """``kv_dtype`` (or ``resident_kv_dtype``, the reference's knob name
         as the scheduler passes it to KV-resident backends) selects the pool
-        dtype: a torch dtype or "fp32" / "fp16" / "bf16". Default: the dtype of
-        the first request's KV. Queries, keys and values are converted to it;
-        outputs come back in each query's dtype."""
+        dtype: a torch dtype or "fp32" / "fp16" / "bf16" / "fp8". Default: the
+        dtype of the first request's KV. Queries, keys and values are converted
+        to it; outputs come back in each query's dtype. "fp8" keeps OCP e4m3
+        pools with ``kv_scale`` (a number or one value per kv head, the same
+        for keys and values): values are stored as e4m3(x / scale), queries
+        and the attention math stay 16-bit / fp32."""
         if num_blocks <= 0 or block_size <= 0 or block_size & (block_size - 1):
             raise ValueError("num_blocks must be positive and block_size a power of two")
         if kv_dtype is not None and resident_kv_dtype is not None and \
@@ -84,6 +89,9 @@ class GpuAttentionBackend:
             raise RuntimeError("GpuAttentionBackend needs a HIP device (there is no CPU fallback)")
         self.kv_dtype = _kv_dtype(kv_dtype if kv_dtype is not None else resident_kv_dtype)
         self.partition_size = partition_size
+        self.kv_scale = kv_scale
+        self.k_scales: Optional[torch.Tensor] = None  # fp8 pools: [num_kv_heads] on the device
+        self.v_scales: Optional[torch.Tensor] = None
         self.k_pools: Optional[torch.Tensor] = None  # [L, NB, bs, Hkv, D]
         self.v_pools: Optional[torch.Tensor] = None
         self.num_layers = 0
@@ -108,9 +116,34 @@ class GpuAttentionBackend:
             return
         dtype = self.kv_dtype or dtype
         shape = (num_layers, self.num_blocks, self.block_size, num_kv_heads, head_dim)
+        if dtype == kernels.FP8:
+            self.k_scales = kernels.kv_scales(self.kv_scale, num_kv_heads, self.device)
+            self.v_scales = self.k_scales
         self.k_pools = torch.zeros(shape, dtype=dtype, device=self.device)
         self.v_pools = torch.zeros(shape, dtype=dtype, device=self.device)
         self.num_layers = num_layers
+
+    @property
+    def _fp8(self) -> bool:
+        return self.k_pools is not None and self.k_pools.dtype == kernels.FP8
+
+    def _append_dtype(self, src: torch.dtype) -> torch.dtype:
+        """dtype new K/V rows are handed to the append in: the pool dtype, or
+        for fp8 pools a float dtype the quantising append reads."""
+        if not self._fp8:
+            return self.k_pools.dtype
+        return src if src in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
+
+    def _compute_dtype(self, qdt: torch.dtype) -> torch.dtype:
+        """dtype of q and out in the kernels: the pool dtype, or for fp8
+        pools fp16 for fp16 queries and bf16 otherwise."""
+        if not self._fp8:
+            return self.k_pools.dtype
+        return torch.float16 if qdt == torch.float16 else torch.bfloat16
+
+    def _append(self, k, v, layer: int, slots: torch.Tensor) -> None:
+        kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots,
+                                  k_scale=self.k_scales, v_scale=self.v_scales)
 
     def _take_blocks(self, n: int, what: str) -> List[int]:
         if len(self.free_blocks) < n:
@@ -139,13 +172,13 @@ class GpuAttentionBackend:
             slots = torch.tensor([self._slot(req, p) for p in range(seq_len)],
                                  dtype=torch.int64).to(self.device)
             for layer, kv in enumerate(initial_kv):
-                k = kv["key"].to(device=self.device, dtype=self.k_pools.dtype)
-                v = kv["value"].to(device=self.device, dtype=self.v_pools.dtype)
+                k = kv["key"].to(device=self.device, dtype=self._append_dtype(kv["key"].dtype))
+                v = kv["value"].to(device=self.device, dtype=k.dtype)
                 if k.shape != (seq_len, hkv, d) or v.shape != k.shape:
                     self.free_blocks.extend(req.blocks)
                     self.tables.remove(req.row)
                     raise ValueError(f"layer {layer}: key/value shape differs from layer 0")
-                kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots)
+                self._append(k, v, layer, slots)
         self.requests[request_id] = req
         self.stats["init_requests"] += 1
         return seq_len
@@ -207,13 +240,13 @@ class GpuAttentionBackend:
                     self.free_blocks.extend(blocks)
                     self.tables.remove(req.row)
                     raise ValueError(f"layer {layer}: key/value shape differs from layer 0")
-                k = k[:T].to(device=self.device, dtype=self.k_pools.dtype)
-                v = v[:T].to(device=self.device, dtype=self.v_pools.dtype)
+                k = k[:T].to(device=self.device, dtype=self._append_dtype(k.dtype))
+                v = v[:T].to(device=self.device, dtype=k.dtype)
                 if k.stride(2) != 1:
                     k = k.contiguous()
                 if v.stride(2) != 1:
                     v = v.contiguous()
-                kernels.reshape_and_cache(k, v, self.k_pools[layer], self.v_pools[layer], slots)
+                self._append(k, v, layer, slots)
         self.requests[request_id] = req
         self.stats["init_requests"] += 1
         return T
@@ -282,16 +315,17 @@ class GpuAttentionBackend:
                   score_scale: float) -> List[torch.Tensor]:
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"layer_idx {layer} outside [0, {self.num_layers})")
-        dt = self.k_pools.dtype
         _, _, bs, hkv, d = self.k_pools.shape
         if self._stage_done is not None:
             self._stage_done.synchronize()  # the staging buffers are free again
         q0 = items[0]["query"]
         hq = q0.numel() // d
         n = len(items)
+        dt = self._compute_dtype(q0.dtype)
         q = self._rows(items, "query", hq, d, dt)
-        k = self._rows(items, "key", hkv, d, dt)
-        v = self._rows(items, "value", hkv, d, dt)
+        kdt = self._append_dtype(items[0]["key"].dtype)  # fp8 pools: quantised once, from the payload
+        k = self._rows(items, "key", hkv, d, kdt)
+        v = self._rows(items, "value", hkv, d, kdt)
 
         # Metadata, one copy: slots (int64), new block-table entries (int64
         # rows / columns / blocks), context lengths and table rows (int32).
@@ -332,9 +366,10 @@ class GpuAttentionBackend:
             kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens), k, v,
                                            scale=score_scale)
         else:
-            kernels.reshape_and_cache(k, v, kp, vp, slots_dev)
+            self._append(k, v, layer, slots_dev)
             kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens),
-                                    scale=score_scale, partition_size=self.partition_size)
+                                    scale=score_scale, partition_size=self.partition_size,
+                                    k_scale=self.k_scales, v_scale=self.v_scales)
         if layer == self.num_layers - 1:
             for req in reqs:
                 req.context_len += 1

@@ -147,6 +147,48 @@ int clv_reshape_and_cache(const clv_cache_args *a, clv_stream_t stream) {
                                                                               : CLV_ELAUNCH;
 }
 
+int clv_reshape_and_cache_fp8(const clv_cache_args *a, const float *k_scales,
+                              const float *v_scales, clv_stream_t stream) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (a->dtype != CLV_F32 && a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
+  if (a->num_tokens < 0 || a->num_kv_heads <= 0 || a->head_dim <= 0 || a->num_blocks <= 0)
+    return CLV_EINVAL;
+  if (!is_pow2(a->block_size)) return CLV_EUNSUPPORTED;
+  if (a->head_dim % 8 != 0) return CLV_EUNSUPPORTED;
+  if (a->num_tokens == 0) return CLV_OK;
+  if (!a->key || !a->value || !a->k_cache || !a->v_cache || !a->slot_mapping || !k_scales ||
+      !v_scales)
+    return CLV_EINVAL;
+  // fp8 pools: one byte per element, rows written 8 bytes at a time.
+  if (((uintptr_t)a->k_cache & 7u) || ((uintptr_t)a->v_cache & 7u) || (a->kv_stride_block & 7) ||
+      (a->kv_stride_token & 7) || (a->kv_stride_head & 7))
+    return CLV_EINVAL;
+  clv::CacheParams p{};
+  p.key = a->key;
+  p.value = a->value;
+  p.k_cache = a->k_cache;
+  p.v_cache = a->v_cache;
+  p.slot_mapping = a->slot_mapping;
+  p.key_stride_token = a->key_stride_token;
+  p.key_stride_head = a->key_stride_head;
+  p.value_stride_token = a->value_stride_token;
+  p.value_stride_head = a->value_stride_head;
+  p.kv_stride_block = a->kv_stride_block;
+  p.kv_stride_token = a->kv_stride_token;
+  p.kv_stride_head = a->kv_stride_head;
+  p.num_tokens = a->num_tokens;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.block_shift = log2_int(a->block_size);
+  p.num_blocks = a->num_blocks;
+  p.num_slots = (int64_t)a->num_blocks * a->block_size;
+  p.elem_bytes = elem_bytes(a->dtype);
+  return clv::launch_reshape_and_cache_fp8(p, a->dtype, k_scales, v_scales, (hipStream_t)stream) ==
+                 hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
+}
+
 int clv_paged_decode(const clv_decode_args *a, clv_stream_t stream) {
   clv::DecodeParams p;
   const int st = fill_decode(a, &p);
@@ -246,6 +288,8 @@ int32_t clv_default_num_waves(void) {
   return cus * 4;
 }
 
+int32_t clv_default_num_waves_fp8(void) { return 2 * clv_default_num_waves(); }
+
 size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                     int32_t head_dim, int32_t num_waves) {
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
@@ -264,13 +308,13 @@ namespace {
 
 // Ring depth of the balanced decode: steps of loads each wave keeps in
 // flight (2, 3, 4 or 6). CLV_STREAM_DEPTH overrides the default for tuning.
-int stream_depth_setting() {
+int stream_depth_setting(int def = 3) {
   const char *env = getenv("CLV_STREAM_DEPTH");
   if (env) {
     const int d = atoi(env);
     if (d == 2 || d == 3 || d == 4 || d == 6) return d;
   }
-  return 3;
+  return def;
 }
 
 // Phantom steps the balanced decode charges for each segment a wave starts
@@ -370,6 +414,31 @@ int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const
   } else if (clv::launch_append_by_table(p, s) != hipSuccess) {
     return CLV_ELAUNCH;
   }
+  if (clv::launch_decode_stream(p, (DType)a->dtype, s) != hipSuccess) return CLV_ELAUNCH;
+  return clv::launch_stream_reduce(p, (DType)a->dtype, s) == hipSuccess ? CLV_OK : CLV_ELAUNCH;
+}
+
+int clv_paged_decode_fp8(const clv_decode_args *a, const float *k_scales, const float *v_scales,
+                         int32_t num_waves, void *workspace, size_t workspace_bytes,
+                         clv_stream_t stream) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
+  if (a->head_dim != 128 || a->block_size < 16) return CLV_EUNSUPPORTED;
+  clv::DecodeParams p;
+  if (num_waves <= 0) num_waves = clv_default_num_waves_fp8();
+  const int st = fill_balanced(a, num_waves, workspace, workspace_bytes, &p);
+  if (st != CLV_OK || p.num_seqs == 0) return st;
+  if (!k_scales || !v_scales) return CLV_EINVAL;
+  // fp8 pools: strides are bytes; each lane reads 8-byte row chunks.
+  if ((a->kv_stride_block & 15) || (a->kv_stride_token & 15) || (a->kv_stride_head & 15))
+    return CLV_EINVAL;
+  // Half the bytes per step make the per-step compute the longer part: two
+  // waves per SIMD (clv_default_num_waves_fp8) with four steps in flight.
+  p.stream_depth = stream_depth_setting(4);
+  p.kv_fp8 = 1;
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
+  const hipStream_t s = (hipStream_t)stream;
   if (clv::launch_decode_stream(p, (DType)a->dtype, s) != hipSuccess) return CLV_ELAUNCH;
   return clv::launch_stream_reduce(p, (DType)a->dtype, s) == hipSuccess ? CLV_OK : CLV_ELAUNCH;
 }

@@ -48,6 +48,11 @@ struct DecodeParams {
   const void *key_new;
   const void *value_new;
   int64_t new_stride_seq, new_stride_head;
+  // fp8 pools (balanced mode): k_cache/v_cache hold OCP e4m3 bytes, strides
+  // in bytes, with one scale per kv head; q and out are f16/bf16.
+  int32_t kv_fp8;
+  const float *k_scales;  // [num_kv_heads]
+  const float *v_scales;  // [num_kv_heads]
 };
 
 // Largest segment count the balanced mode keeps in LDS.
@@ -97,6 +102,10 @@ hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t str
 // sequence (slot from its block table), for the decode shapes whose stream
 // kernel does not append itself.
 hipError_t launch_append_by_table(const DecodeParams &p, hipStream_t stream);
+// KV append into fp8 (OCP e4m3) pools: cache = e4m3(clamp(x / scale[h], +-448)),
+// rounded to nearest even; key/value in CacheParams' elem_bytes (2 or 4).
+hipError_t launch_reshape_and_cache_fp8(const CacheParams &p, int src_dtype, const float *k_scales,
+                                        const float *v_scales, hipStream_t stream);
 hipError_t launch_prefill_valu(const PrefillParams &p, DType dt, hipStream_t stream);
 
 // Whether the MFMA decode kernel covers this shape/dtype.

@@ -50,13 +50,14 @@ struct SegGeom {
   int t_end;  // tokens [.., t_end) are attended
 };
 
-template <typename T>
+// CEB: bytes per cache element (sizeof(T), or 1 for fp8 pools).
+template <typename T, int CEB = (int)sizeof(T)>
 __device__ __forceinline__ SegGeom seg_geom(const DecodeParams &p, int s, int kvh, int t_end,
                                            const int32_t *__restrict__ tables) {
   SegGeom g;
   g.bt = tables + (int64_t)s * p.max_blocks_per_seq;
-  g.kbase = (const char *)p.k_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
-  g.vbase = (const char *)p.v_cache + (int64_t)kvh * p.kv_stride_head * (int64_t)sizeof(T);
+  g.kbase = (const char *)p.k_cache + (int64_t)kvh * p.kv_stride_head * CEB;
+  g.vbase = (const char *)p.v_cache + (int64_t)kvh * p.kv_stride_head * CEB;
   g.t_end = t_end;
   return g;
 }
@@ -79,6 +80,26 @@ __device__ __forceinline__ void kt_store_row(const char *kbase, const char *vbas
   }
 }
 
+// Eight fp8 (OCP e4m3) values, bytes of w in order, as eight T values (exact
+// for both 16-bit types: e4m3 has 3 mantissa bits and an exponent range
+// inside theirs).
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8_to(u32x2 w) {
+  u32x4 r;
+  if constexpr (__is_same(T, __bf16)) {
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0], 1.f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[1], 1.f, true));
+  } else {
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.f, false));
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0], 1.f, true));
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.f, false));
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[1], 1.f, true));
+  }
+  return r;
+}
+
 // UNI: block_size >= 16, so a step sits in one block and its block-table
 // entry is wave-uniform (scalar load, buffer loads). Otherwise (block_size 4
 // or 8) lanes look up their own rows.
@@ -87,7 +108,12 @@ __device__ __forceinline__ void kt_store_row(const char *kbase, const char *vbas
 // layout through a per-wave LDS buffer of 16 rows (set_k_lds). A pure read of
 // that pattern runs about 3 % faster than the A-layout loads, which read half
 // of each 128-byte line per instruction.
-template <typename T, int D, bool UNI, bool KT = false>
+// KV8 (KT only): the pools hold fp8 (OCP e4m3) values with a scale per kv
+// head. Each lane loads the same rows as in the 16-bit case at half the width
+// (8 bytes = 8 values) and converts them exactly to T in registers; the key
+// scale is folded into the softmax scale and the value scale into the
+// partial context (set_kv_scales).
+template <typename T, int D, bool UNI, bool KT = false, bool KV8 = false>
 struct DecodeWave {
   typedef Mfma16x16x32<T> MfK;
   typedef Mfma16x16x16<T> MfV;
@@ -102,12 +128,15 @@ struct DecodeWave {
   static constexpr int KT_ROW = D * EB + 32;
   static constexpr int KT_BYTES = 16 * KT_ROW;
   static_assert(!KT || (UNI && D == 128), "K transpose needs block_size >= 16 and head_dim 128");
+  static_assert(!KV8 || KT, "fp8 pools are read on the K-transpose path");
+  static constexpr int EBC = KV8 ? 1 : EB;  // bytes per cache element
   typedef typename VChunk<CH>::type vchunk_t;
 
   // Loads of one step: K rows (lane row n16) and the V rows 4j..4j+3.
   struct Regs {
     u32x4 k[NQK];
     vchunk_t v[4];
+    u32x2 k8[KV8 ? NQK : 1], v8[KV8 ? 4 : 1];  // KV8: the loaded fp8 values
     bool ok;  // the lane's V rows lie in a readable block
   };
 
@@ -122,21 +151,30 @@ struct DecodeWave {
   f32x4 o[CH];         // O[g = 4j + r][d = n16 * CH + m]
   float m_run;         // running max of row g = n16 (log2 domain)
   float l_run;         // this lane's share of the row sum
+  float vscale;        // KV8: value scale of the kv head
 
   __device__ __forceinline__ void init(const DecodeParams &p) {
     const int lane = threadIdx.x & 63;
     n16 = lane & 15;
     j = lane >> 4;
-    sblk = p.kv_stride_block * EB;
-    stok = p.kv_stride_token * EB;
+    sblk = p.kv_stride_block * EBC;
+    stok = p.kv_stride_token * EBC;
     bshift = p.block_shift;
     bmask = (1 << bshift) - 1;
     nblocks = (unsigned)p.num_blocks;
     scale_log2 = p.scale_log2;
     k_lane = (uint32_t)(n16 * stok + 8 * j * EB);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) v_lane[r] = (uint32_t)((4 * j + r) * stok + n16 * CH * EB);
+    for (int r = 0; r < 4; ++r) v_lane[r] = (uint32_t)((4 * j + r) * stok + n16 * CH * EBC);
+    vscale = 1.f;
     reset();
+  }
+
+  // KV8: the scales of the kv head a run reads (the key scale times the
+  // softmax scale in the log2 domain, and the value scale).
+  __device__ __forceinline__ void set_kv_scales(float scale_log2_k, float vs) {
+    scale_log2 = scale_log2_k;
+    vscale = vs;
   }
 
   __device__ __forceinline__ void reset() {
@@ -182,7 +220,13 @@ struct DecodeWave {
     R.ok = ok;
     const rsrc_t rk = make_rsrc(kbase + off);
     const rsrc_t rv = make_rsrc(vbase + off);
-    if constexpr (KT) {
+    if constexpr (KV8) {
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) R.k8[i] = buf_load<u32x2, kCacheStream>(rk, v_lane[i]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R.v8[r] = buf_load<u32x2, kCacheStream>(rv, v_lane[r]);
+      return;
+    } else if constexpr (KT) {
 #pragma unroll
       for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4, kCacheStream>(rk, v_lane[i]);
     } else {
@@ -220,6 +264,14 @@ struct DecodeWave {
 
   // Fold the step starting at `base` into (o, m_run, l_run).
   __device__ __forceinline__ void compute(int base, int t_end, Regs &R, const qk_t (&q)[NQK]) {
+    if constexpr (KV8) {
+      // fp8 -> T, exact: eight values per row chunk, the layout of the
+      // 16-bit loads.
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) R.k[i] = fp8x8_to<T>(R.k8[i]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) R.v[r] = __builtin_bit_cast(vchunk_t, fp8x8_to<T>(R.v8[r]));
+    }
     if constexpr (KT) {
       // R.k[i] holds row 4j + i, bytes 16 n16 .. +16 (the V pattern). Through
       // LDS into the A layout: row n16, bytes 64 i + 16 j .. +16. A wave's LDS
@@ -303,7 +355,7 @@ struct DecodeWave {
       const float l = shfl(l_run, g);
       const float mrow = shfl(m_run, g);
       if (g >= ng) continue;
-      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const float inv = (l > 0.f ? 1.f / l : 0.f) * (KV8 ? vscale : 1.f);
       float *dst = ws_o + (row0 + g) * D + n16 * CH;
 #pragma unroll
       for (int m = 0; m < CH; m += 4) {

@@ -73,7 +73,8 @@ __device__ int block_exclusive_scan(int *buf, int n, int *tmp) {
 }
 
 // APPEND (K-transpose path only): fused append, see below.
-template <typename T, int D, bool UNI, int DEPTH, bool APPEND = false>
+// KV8 (K-transpose path only): fp8 pools, see DecodeWave.
+template <typename T, int D, bool UNI, int DEPTH, bool APPEND = false, bool KV8 = false>
 __global__ void __launch_bounds__(kThreads)
 paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
                     const int32_t *__restrict__ lens, float *__restrict__ ws_o,
@@ -82,7 +83,8 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   // Every global pointer is a separate restrict argument: with stores to the
   // workspace inside the main loop, that is what lets the compiler keep the
   // wave-uniform block-table reads scalar loads.
-  typedef DecodeWave<T, D, UNI, UNI && D == 128> WV;
+  typedef DecodeWave<T, D, UNI, UNI && D == 128, KV8> WV;
+  constexpr int CEB = KV8 ? 1 : (int)sizeof(T);
   typedef typename WV::qk_t qk_t;
   __shared__ __attribute__((aligned(16))) char s_kt[kWaves][WV::KT_BYTES];
   __shared__ int s_seg[kStreamMaxSegments + 1];
@@ -186,7 +188,12 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     const int g0 = (rem - kvh * p.n_gchunks) * 16;
     const int ng = min(16, p.group - g0);
     const int ctx = clamp_ctx(p, lens, s_);
-    const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
+    const SegGeom geo = seg_geom<T, CEB>(p, s_, kvh, ctx, tables);
+    if constexpr (KV8) {  // the kv head's scales (wave-uniform, scalar loads)
+      const float ks = __builtin_bit_cast(float, scalar_load_i32((const int32_t *)p.k_scales + kvh));
+      const float vs = __builtin_bit_cast(float, scalar_load_i32((const int32_t *)p.v_scales + kvh));
+      w.set_kv_scales(p.scale_log2 * ks, vs);
+    }
 
     // Q loads go out first and are waited for only after the ring below is
     // issued, so a run start costs one memory latency, not two.
@@ -265,6 +272,13 @@ template <typename T, int D, int DEPTH>
 hipError_t launch_stream_tdd(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((p.num_waves + kWaves - 1) / kWaves));
   if constexpr (D == 128) {
+    if (p.kv_fp8) {  // validated: block_size >= 16, no fused append
+      if (p.block_shift < 4 || p.append_new) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, false, true>), grid, dim3(kThreads),
+                         0, stream, p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l,
+                         p.seg_prefix, p.slot_prefix);
+      return hipGetLastError();
+    }
     if (p.append_new) {  // set only where stream_appends_in_kernel holds
       if (p.block_shift < 4) return hipErrorInvalidValue;
       hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, true>), grid, dim3(kThreads), 0,

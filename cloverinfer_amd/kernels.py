@@ -29,6 +29,29 @@ _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _num_cus: dict[int, int] = {}
 
 
+# fp8 pool dtype: OCP e4m3 (the format gfx950's conversions use), one scale
+# per kv head.
+FP8 = torch.float8_e4m3fn
+
+
+def kv_scales(scale, num_kv_heads: int, device: torch.device) -> torch.Tensor:
+    """Per-kv-head fp32 scales of an fp8 pool as a device tensor: a number (the
+    same for every head), a sequence or a tensor of num_kv_heads values."""
+    if scale is None:
+        raise ValueError("fp8 pools need k_scale and v_scale")
+    if isinstance(scale, torch.Tensor) and scale.device == device and \
+            scale.dtype == torch.float32 and scale.shape == (num_kv_heads,) and scale.is_contiguous():
+        return scale  # already a device tensor (not re-validated: that would synchronise)
+    t = torch.as_tensor(scale, dtype=torch.float32, device="cpu")
+    if t.dim() == 0:
+        t = t.expand(num_kv_heads)
+    if t.shape != (num_kv_heads,):
+        raise ValueError(f"scales must be a number or [{num_kv_heads}] values")
+    if not bool(torch.isfinite(t).all()) or not bool((t > 0).all()):
+        raise ValueError("scales must be positive and finite")
+    return t.to(device=device).contiguous()
+
+
 def _dtype_code(t: torch.Tensor) -> int:
     try:
         return _DTYPES[t.dtype]
@@ -116,8 +139,11 @@ def _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_siz
         raise ValueError(f"block_size {block_size} does not match the cache ({bs})")
     if num_heads % num_kv_heads:
         raise ValueError(f"num_heads {num_heads} is not a multiple of num_kv_heads {num_kv_heads}")
-    if q.dtype != k_cache.dtype or out.dtype != q.dtype:
+    fp8 = k_cache.dtype == FP8
+    if out.dtype != q.dtype or (q.dtype != k_cache.dtype and not fp8):
         raise ValueError("q, out and the caches must share one dtype")
+    if fp8 and q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("fp8 pools need float16 or bfloat16 queries")
     if q.stride(2) != 1 or out.stride(2) != 1:
         raise ValueError("q and out need a contiguous head_dim")
     if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
@@ -174,7 +200,7 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_tables: torch.Tensor,
                     context_lens: torch.Tensor, block_size: int, max_context_len: int,
                     scale: float | None = None, partition_size: int | None = None,
-                    num_waves: int = 0) -> None:
+                    num_waves: int = 0, k_scale=None, v_scale=None) -> None:
     """``out[s,h] = softmax(scale * q[s,h] . K^T) V`` over each sequence's paged context.
 
     Same arguments as the reference op (src/kernels/csrc/manager.cpp:19-27);
@@ -184,12 +210,29 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     with ``num_waves`` waves, 0 = the device default), 0 forces a single
     pass per (sequence, kv head), a positive multiple of 32 forces split-K
     with that many tokens per partition.
+
+    fp8 pools (``k_cache.dtype == FP8``): K = e4m3 * ``k_scale``, V = e4m3 *
+    ``v_scale`` (numbers or per-kv-head values), balanced schedule only
+    (head_dim 128, block_size >= 16), ``partition_size`` must be None.
     """
     dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens)
     a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
                      max_context_len, scale)
     lib = _native.load()
     stream = _stream(dev)
+    if k_cache.dtype == FP8:
+        if partition_size is not None:
+            raise ValueError("fp8 pools use the balanced schedule (partition_size=None)")
+        ks = kv_scales(k_scale, a.num_kv_heads, dev)
+        vs = kv_scales(v_scale, a.num_kv_heads, dev)
+        num_waves = num_waves or lib.clv_default_num_waves_fp8()
+        nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
+                                                  a.head_dim, num_waves)
+        ws = splitk_workspace(dev, nbytes)
+        _native.check(lib.clv_paged_decode_fp8(a, ks.data_ptr(), vs.data_ptr(), num_waves,
+                                               ws.data_ptr(), ws.numel(), stream),
+                      "clv_paged_decode_fp8")
+        return
     if partition_size is None:
         if balanced_supported(a):
             nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
@@ -298,9 +341,12 @@ def splitk_reduce(a: _native.DecodeArgs, partition_size: int, workspace: torch.T
 
 
 def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
-                      v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                      k_scale=None, v_scale=None) -> None:
     """Write token i's ``key[i]``/``value[i]`` ([num_kv_heads, head_dim]) to cache slot
-    ``slot_mapping[i]`` (= block*block_size + offset; negative slots are skipped)."""
+    ``slot_mapping[i]`` (= block*block_size + offset; negative slots are skipped).
+    fp8 pools store e4m3(clamp(x / scale, -448, 448)) with per-kv-head
+    ``k_scale``/``v_scale``."""
     dev = _require_device(key, value, k_cache, v_cache, slot_mapping)
     _check_cache(k_cache, v_cache)
     num_blocks, bs, num_kv_heads, head_dim = k_cache.shape
@@ -309,7 +355,8 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
             f"key/value must be [num_tokens, {num_kv_heads}, {head_dim}], got "
             f"{tuple(key.shape)} and {tuple(value.shape)}"
         )
-    if key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
+    fp8 = k_cache.dtype == FP8
+    if value.dtype != key.dtype or (key.dtype != k_cache.dtype and not fp8):
         raise ValueError("key/value dtype must match the cache dtype")
     if key.stride(2) != 1 or value.stride(2) != 1:
         raise ValueError("key/value need a contiguous head_dim")
@@ -325,7 +372,14 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     a.kv_stride_block, a.kv_stride_token, a.kv_stride_head = k_cache.stride()[:3]
     a.num_tokens = key.shape[0]
     a.num_kv_heads, a.head_dim, a.block_size, a.num_blocks = num_kv_heads, head_dim, bs, num_blocks
-    a.dtype = _dtype_code(k_cache)
+    a.dtype = _dtype_code(key)
+    if fp8:
+        ks = kv_scales(k_scale, num_kv_heads, dev)
+        vs = kv_scales(v_scale, num_kv_heads, dev)
+        _native.check(_native.load().clv_reshape_and_cache_fp8(a, ks.data_ptr(), vs.data_ptr(),
+                                                               _stream(dev)),
+                      "clv_reshape_and_cache_fp8")
+        return
     _native.check(_native.load().clv_reshape_and_cache(a, _stream(dev)), "clv_reshape_and_cache")
 
 
@@ -347,8 +401,11 @@ def chunked_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     num_blocks, bs, num_kv_heads, kd = k_cache.shape
     if kd != head_dim or num_heads % num_kv_heads:
         raise ValueError("q and the caches disagree on head_dim or the GQA grouping")
-    if q.dtype != k_cache.dtype or out.dtype != q.dtype:
+    fp8 = k_cache.dtype == FP8
+    if out.dtype != q.dtype or (q.dtype != k_cache.dtype and not fp8):
         raise ValueError("q, out and the caches must share one dtype")
+    if fp8 and q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("fp8 pools need float16 or bfloat16 queries")
     if q.stride(2) != 1 or out.stride(2) != 1:
         raise ValueError("q and out need a contiguous head_dim")
     num_seqs = context_lens.shape[0]

@@ -228,6 +228,35 @@ int clv_paged_decode_append(const clv_decode_args *args, const void *key_new,
                             void *workspace, size_t workspace_bytes,
                             clv_stream_t stream);
 
+/*
+ * fp8 KV pools (OCP e4m3, one byte per element, a float32 scale per kv head;
+ * the reference keeps its resident KV in fp32 or fp16, the pool dtype knob of
+ * src/core/config.py:38, and has no fp8 form). A stored byte b stands for
+ * e4m3(b) * scale[kv head].
+ *
+ * Append: like clv_reshape_and_cache, with the pools in fp8 (kv strides in
+ * bytes, multiples of 8, 8-byte aligned pools, head_dim a multiple of 8);
+ * `dtype` is the dtype of key/value. Each value is stored as
+ *     e4m3(clamp(x / scale[h], -448, 448)), rounded to nearest even
+ * (NaN stays NaN).
+ */
+int clv_reshape_and_cache_fp8(const clv_cache_args *args, const float *k_scales,
+                              const float *v_scales, clv_stream_t stream);
+
+/*
+ * Balanced decode over fp8 pools: the result of clv_paged_decode_balanced
+ * with K = e4m3(k) * k_scales[h] and V = e4m3(v) * v_scales[h] (exact
+ * conversion; the key scale is folded into the softmax scale, the value scale
+ * into each partial context). `dtype` is that of q and out (f16 or bf16);
+ * kv strides are in bytes (multiples of 16); head_dim 128, block_size >= 16.
+ * Workspace as clv_paged_decode_balanced, sized for the wave count used:
+ * num_waves <= 0 picks clv_default_num_waves_fp8(). No counterpart in the
+ * reference.
+ */
+int clv_paged_decode_fp8(const clv_decode_args *args, const float *k_scales,
+                         const float *v_scales, int32_t num_waves, void *workspace,
+                         size_t workspace_bytes, clv_stream_t stream);
+
 /* Workspace bytes of clv_paged_decode_balanced (num_waves <= 0: default). */
 size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads,
                                     int32_t num_kv_heads, int32_t head_dim,
@@ -235,6 +264,9 @@ size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads,
 
 /* Default wave count of the balanced decode on the current device. */
 int32_t clv_default_num_waves(void);
+
+/* Default wave count of clv_paged_decode_fp8 (two per SIMD). */
+int32_t clv_default_num_waves_fp8(void);
 
 /*
  * Chunked prefill over paged KV (MFMA for fp16/bf16). No counterpart in the

@@ -92,6 +92,55 @@ def split_attend(q: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
     return lse_merge(parts)
 
 
+# fp8 pools (OCP e4m3, torch.float8_e4m3fn): a stored byte b stands for
+# e4m3(b) * scale of its kv head. The reference has no fp8 pool (its resident
+# KV dtypes are fp32 and fp16, src/core/attention_backend.py:201); this is the
+# definition the fp8 kernels are checked against.
+E4M3_MAX = 448.0
+
+
+def quantize_fp8(x: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``x`` [..., H, D] (any float dtype) -> float8_e4m3fn codes of
+    clamp(x / scale[h], -448, 448) rounded to nearest even; NaN becomes the
+    positive NaN code 0x7f. The division is fp32 and correctly rounded."""
+    y = x.float() / scale.float().view(-1, 1)
+    y = torch.where(y > E4M3_MAX, torch.full_like(y, E4M3_MAX),
+                    torch.where(y < -E4M3_MAX, torch.full_like(y, -E4M3_MAX), y))
+    codes = y.to(torch.float8_e4m3fn).view(torch.uint8)
+    codes = torch.where(torch.isnan(y), torch.full_like(codes, 0x7F), codes)
+    return codes.view(torch.float8_e4m3fn)
+
+
+def dequantize_fp8(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """fp32 values of fp8 codes [..., H, D] with per-head ``scale``."""
+    return codes.float() * scale.float().view(-1, 1)
+
+
+def e4m3_value(code: int) -> float:
+    """Value of one OCP e4m3 byte from its fields (sign, 4-bit exponent of
+    bias 7, 3-bit mantissa; exponent 0 is subnormal; 0x7f/0xff are NaN)."""
+    sign = -1.0 if code & 0x80 else 1.0
+    e, m = (code >> 3) & 0xF, code & 0x7
+    if e == 0xF and m == 0x7:
+        return math.nan
+    if e == 0:
+        return sign * m * 2.0 ** -9
+    return sign * (1 + m / 8) * 2.0 ** (e - 7)
+
+
+def e4m3_round(x: float) -> int:
+    """e4m3 code of a finite |x| <= 448: the sign bit of x, then the nearest
+    non-negative code, ties to the even one (brute force over the table)."""
+    sign = 0x80 if math.copysign(1.0, x) < 0 else 0
+    a = abs(x)
+    best = None
+    for c in range(0x7F):  # the non-negative finite codes, in increasing value
+        d = abs(e4m3_value(c) - a)
+        if best is None or d < best[0] or (d == best[0] and (c & 1) == 0):
+            best = (d, c)
+    return sign | best[1]
+
+
 def gather_context(k_cache: torch.Tensor, v_cache: torch.Tensor, blocks: Sequence[int],
                    context_len: int):
     """Contiguous ``[L, Hkv, D]`` K/V of one sequence from paged pools

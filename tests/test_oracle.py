@@ -216,3 +216,33 @@ def test_block_bookkeeping_errors_and_free_order():
     bk.free("nope")
     tables, lens, mx = bk.kernel_inputs(["b"])
     assert tables == [[1, 0]] and lens == [4] and mx == 4
+
+
+def test_fp8_codes_and_rounding_pinned():
+    """The fp8 pool definition: torch's float8_e4m3fn decode equals the e4m3
+    field formula on all 256 codes, and its encode (after the clamp) equals
+    the brute-force nearest-even search on values that include every
+    representable value, every midpoint between neighbours, signed zeros,
+    subnormals, values that round to zero and out-of-range magnitudes."""
+    import math
+    codes = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    for c in range(256):
+        want = oa.e4m3_value(c)
+        assert (math.isnan(want) and math.isnan(codes[c].item())) or codes[c].item() == want
+    finite = sorted({oa.e4m3_value(c) for c in range(256) if not math.isnan(oa.e4m3_value(c))})
+    mids = [(a + b) / 2 for a, b in zip(finite, finite[1:])]
+    g = torch.Generator().manual_seed(5)
+    rand = (torch.randn(400, generator=g) * torch.tensor([0.003, 0.1, 3.0, 300.0]).repeat(100)).tolist()
+    vals = finite + mids + [-0.0, 0.0, 2.0 ** -10, -2.0 ** -10, 3 * 2.0 ** -11, 500.0, -1e6] + rand
+    x = torch.tensor(vals, dtype=torch.float32)
+    got = oa.quantize_fp8(x.view(-1, 1, 1), torch.ones(1)).view(torch.uint8).flatten().tolist()
+    for v, c in zip(vals, got):
+        assert c == oa.e4m3_round(max(-448.0, min(448.0, v))), (v, hex(c))
+    # scales divide, per kv head; NaN becomes code 0x7f; dequantize inverts exact codes
+    s = torch.tensor([0.5, 4.0])
+    q = oa.quantize_fp8(torch.tensor([[[1.0, float("nan")], [6.0, -1e9]]]), s)
+    assert q.float()[0, 0, 0].item() == 2.0 and q.view(torch.uint8)[0, 0, 1].item() == 0x7F
+    neg_nan = oa.quantize_fp8(-torch.tensor([[[float("nan")]]]), torch.ones(1))
+    assert neg_nan.view(torch.uint8).item() == 0x7F
+    assert q.float()[0, 1].tolist() == [1.5, -448.0]
+    assert torch.equal(oa.dequantize_fp8(q[:, :, :1], s), torch.tensor([[[1.0], [6.0]]]))

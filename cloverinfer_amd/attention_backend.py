@@ -300,8 +300,19 @@ class GpuAttentionBackend:
         device tensor [B, heads, d], through one copy."""
         ts = [it[name] for it in items]
         n = len(ts)
-        shape = ts[0].shape
-        same = all(t.shape == shape for t in ts) and ts[0].numel() == heads * d
+        t0 = ts[0]
+        if t0.device.type == "cpu" and t0.numel() == heads * d:
+            # The node's case (host tensors of one shape): one stack straight
+            # into the pinned buffer; torch checks shapes and devices itself
+            # (and converts dtypes), anything else takes the general path.
+            host = self._staging(name, (n, heads, d), dt)
+            try:
+                torch.stack(ts, out=host.view(n, *t0.shape))
+                return host.to(self.device, non_blocking=True)
+            except (RuntimeError, TypeError):
+                pass
+        shape = t0.shape
+        same = all(t.shape == shape for t in ts) and t0.numel() == heads * d
         if same and all(t.device == self.device for t in ts):
             return torch.stack(ts).view(n, heads, d).to(dt)
         host = self._staging(name, (n, heads, d), dt)
@@ -381,7 +392,7 @@ class GpuAttentionBackend:
         if len(want) == 1:
             dev, qdt = want.pop()
             res = ctx_out.to(device=dev, dtype=qdt)
-            return [res[i:i + 1] for i in range(n)]
+            return list(res.split(1))
         return [ctx_out[i:i + 1].to(device=it["query"].device, dtype=it["query"].dtype)
                 for i, it in enumerate(items)]
 

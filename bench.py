@@ -513,8 +513,10 @@ def bench_node(args):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The GPU clock ramps up over the first tens of milliseconds of a run:
+    # 200 untimed steps (about 40 ms of decode) reach the steady clock.
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="qwen7b",
                     choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node"])
     ap.add_argument("--partition", type=int, default=None,

@@ -299,7 +299,7 @@ size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t
   const int64_t group = num_heads / num_kv_heads;
   const size_t nseg = (size_t)num_seqs * (size_t)num_kv_heads * (size_t)ceil_div(group, 16);
   const size_t rows = ((size_t)num_waves + nseg) * 16;
-  return 2 * round256((nseg + 1) * 4) + 2 * round256(rows * 4) + round256(rows * (size_t)head_dim * 4);
+  return round256((nseg + 1) * 4) + 2 * round256(rows * 4) + round256(rows * (size_t)head_dim * 4);
 }
 
 }  // extern "C"
@@ -352,8 +352,6 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   p->stream_run_cost = stream_run_cost_setting();
   p->num_segments = (int32_t)nseg;
   p->seg_prefix = (int32_t *)ws;
-  ws += round256(((size_t)nseg + 1) * 4);
-  p->slot_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);
   p->ws_m = (float *)ws;
   ws += round256(rows * 4);

@@ -79,7 +79,7 @@ __global__ void __launch_bounds__(kThreads)
 paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
                     const int32_t *__restrict__ lens, float *__restrict__ ws_o,
                     float *__restrict__ ws_m, float *__restrict__ ws_l,
-                    int32_t *__restrict__ seg_prefix, int32_t *__restrict__ slot_prefix) {
+                    int32_t *__restrict__ seg_prefix) {
   // Every global pointer is a separate restrict argument: with stores to the
   // workspace inside the main loop, that is what lets the compiler keep the
   // wave-uniform block-table reads scalar loads.
@@ -88,7 +88,6 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   typedef typename WV::qk_t qk_t;
   __shared__ __attribute__((aligned(16))) char s_kt[kWaves][WV::KT_BYTES];
   __shared__ int s_seg[kStreamMaxSegments + 1];
-  __shared__ int s_slot[kStreamMaxSegments + 1];
   __shared__ int s_tmp[kWaves];
 
   const int nseg = p.num_segments;
@@ -103,21 +102,8 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   // At most one wave per step, so that every wave owns at least one step and
   // each segment's partials come from consecutive waves.
   const int64_t W = min((int64_t)p.num_waves, N);
-  if (N > 0) {
-    for (int i = threadIdx.x; i < nseg; i += kThreads) {
-      const int a = s_seg[i] + K, b = s_seg[i + 1];  // real steps of segment i
-      s_slot[i] = b > a ? wave_of(b - 1, W, N) - wave_of(a, W, N) + 1 : 0;
-    }
-  } else {
-    for (int i = threadIdx.x; i < nseg; i += kThreads) s_slot[i] = 0;
-  }
-  __syncthreads();
-  block_exclusive_scan(s_slot, nseg, s_tmp);
   if (blockIdx.x == 0) {
-    for (int i = threadIdx.x; i <= nseg; i += kThreads) {
-      seg_prefix[i] = s_seg[i];
-      slot_prefix[i] = s_slot[i];
-    }
+    for (int i = threadIdx.x; i <= nseg; i += kThreads) seg_prefix[i] = s_seg[i];
   }
 
   const int wid = (int)blockIdx.x * kWaves + uni(threadIdx.x >> 6);
@@ -239,8 +225,11 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     }
 
     w.reduce_rowsum();
-    const int piece = wid - wave_of(first, W, N);
-    const int64_t row0 = ((int64_t)uni(s_slot[seg]) + piece) * 16;
+    // Partial slot of the (segment, wave) pair: seg + wid. Along the
+    // flattened steps every change of segment or wave raises seg + wid, so
+    // the slots are distinct and fit the workspace's num_waves + nseg rows;
+    // the merge finds a segment's partials at seg + (its first wave) onwards.
+    const int64_t row0 = ((int64_t)seg + wid) * 16;
     w.store_partial(ws_o, ws_m, ws_l, row0, ng);
     w.reset();
     x = last + 1;
@@ -263,7 +252,7 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int64_t W = min((int64_t)p.num_waves, N);
   int n = 0;
   if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
-  const int64_t row0 = (int64_t)p.slot_prefix[seg] * 16 + g;
+  const int64_t row0 = (n > 0 ? ((int64_t)seg + wave_of(a, W, N)) * 16 : 0) + g;
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
   lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16, 16 * D, n, dst, nullptr);
 }
@@ -276,25 +265,23 @@ hipError_t launch_stream_tdd(const DecodeParams &p, hipStream_t stream) {
       if (p.block_shift < 4 || p.append_new) return hipErrorInvalidValue;
       hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, false, true>), grid, dim3(kThreads),
                          0, stream, p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l,
-                         p.seg_prefix, p.slot_prefix);
+                         p.seg_prefix);
       return hipGetLastError();
     }
     if (p.append_new) {  // set only where stream_appends_in_kernel holds
       if (p.block_shift < 4) return hipErrorInvalidValue;
       hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, true>), grid, dim3(kThreads), 0,
                          stream, p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l,
-                         p.seg_prefix, p.slot_prefix);
+                         p.seg_prefix);
       return hipGetLastError();
     }
   }
   if (p.block_shift >= 4)
     hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH>), grid, dim3(kThreads), 0, stream,
-                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix,
-                       p.slot_prefix);
+                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix);
   else
     hipLaunchKernelGGL((paged_decode_stream<T, D, false, DEPTH>), grid, dim3(kThreads), 0, stream,
-                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix,
-                       p.slot_prefix);
+                       p, p.block_tables, p.context_lens, p.ws_o, p.ws_m, p.ws_l, p.seg_prefix);
   return hipGetLastError();
 }
 

@@ -101,6 +101,15 @@ def decode_workload(cfg, dev):
                 flops=4 * sum(ctx) * cfg["hq"] * cfg["d"], dtype=dtype, scale=cfg["d"] ** -0.5)
 
 
+def _event_us(ev, a: int, b: int):
+    """Mean and median, in microseconds, of the intervals between events a and
+    b of every timed step (the mean is what the roofline divides by)."""
+    d = sorted(e[a].elapsed_time(e[b]) * 1e3 for e in ev)
+    n = len(d)
+    med = d[n // 2] if n % 2 else 0.5 * (d[n // 2 - 1] + d[n // 2])
+    return sum(d) / n, med
+
+
 def cpu_baseline(cfg, w, budget_s: float):
     """The oracle's restatement of CpuAttentionBackend (fp32 upcast, grouped
     einsum, softmax, einsum) over the batch's sequences on the host cores."""
@@ -245,8 +254,8 @@ def bench_decode(args, cfg):
         second_half()
         e[2].record(stream)
     torch.cuda.synchronize()
-    dec_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
-    red_us = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev) * 1e3
+    dec_us, dec_med = _event_us(ev, 0, 1)
+    red_us, red_med = _event_us(ev, 1, 2)
     log(f"step {ms:.4f} ms, decode kernel {dec_us:.1f} us, reduce {red_us:.1f} us")
 
     value = w["algo_bytes"] / (ms * 1e-3) / 1e9
@@ -286,6 +295,7 @@ def bench_decode(args, cfg):
         "tokens_per_s": len(w["ctx"]) / (ms * 1e-3),
         "hbm_frac_of_peak": value / PEAK_HBM_GBS,
         "kernels_us": {"paged_decode": dec_us, "merge": red_us},
+        "kernels_us_median": {"paged_decode": dec_med, "merge": red_med},
         "roofline": {
             "bound": "hbm",
             "kernel": {"balanced": "paged_decode_stream", "split": "paged_decode_mfma",
@@ -350,7 +360,7 @@ def bench_decode_fp8(args):
         step()
         e[1].record(stream)
     torch.cuda.synchronize()
-    call_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
+    call_us, call_med = _event_us(ev, 0, 1)
     ctx = w["ctx"]
     kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * 1 * 2
     qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * 2 * 2
@@ -370,6 +380,7 @@ def bench_decode_fp8(args):
                    "seed": cfg["seed"]},
         "tokens_per_s": len(ctx) / (ms * 1e-3),
         "kernels_us": {"paged_decode_fp8_with_merge": call_us},
+        "kernels_us_median": {"paged_decode_fp8_with_merge": call_med},
         "roofline": {"bound": "hbm", "kernel": "paged_decode_stream (fp8) + merge",
                      "achieved": algo / (call_us * 1e-6) / 1e9, "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": algo / (call_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
@@ -431,8 +442,8 @@ def bench_prefill(args):
         attend()
         e[2].record(stream)
     torch.cuda.synchronize()
-    app_us = sum(e[0].elapsed_time(e[1]) for e in ev) / len(ev) * 1e3
-    att_us = sum(e[1].elapsed_time(e[2]) for e in ev) / len(ev) * 1e3
+    app_us, app_med = _event_us(ev, 0, 1)
+    att_us, att_med = _event_us(ev, 1, 2)
     flops = 4 * d * hq * S * sum(cached + i + 1 for i in range(new))
     achieved = flops / (att_us * 1e-6) / 1e12
     return {
@@ -447,6 +458,7 @@ def bench_prefill(args):
                    "flops_per_step": flops},
         "tokens_per_s": S * new / (ms * 1e-3),
         "kernels_us": {"reshape_and_cache": app_us, "chunked_prefill": att_us},
+        "kernels_us_median": {"reshape_and_cache": app_med, "chunked_prefill": att_med},
         "roofline": {"bound": "mfma", "kernel": "chunked_prefill", "achieved": achieved,
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},

@@ -9,8 +9,8 @@
 // and 2 x D/16 MFMAs 16x16x16 for O[g, d] += P[g, t] V[t, d]. The A operand
 // of the second product is exactly the lane's 4 P values (split into a
 // 16-bit value and its 16-bit rounding residual, so P.V keeps fp32-level
-// accuracy); its B operand for output column block m is element m of the
-// lane's 4 V row chunks, regrouped with v_perm. Loads go through buffer
+// accuracy; over fp8 pools one fp16 value); its B operand for output column
+// block m is element m of the lane's 4 V row chunks, regrouped with v_perm. Loads go through buffer
 // resources (a wave-uniform base in SGPRs plus 32-bit lane offsets). V rows
 // are read whole by each instruction and once per kv head, so they use the
 // streaming cache policy; a K instruction reads half of each 128-byte line
@@ -265,12 +265,14 @@ struct DecodeWave {
   // Fold the step starting at `base` into (o, m_run, l_run).
   __device__ __forceinline__ void compute(int base, int t_end, Regs &R, const qk_t (&q)[NQK]) {
     if constexpr (KV8) {
-      // fp8 -> T, exact: eight values per row chunk, the layout of the
-      // 16-bit loads.
+      // fp8 -> 16 bits, exact, eight values per row chunk (the layout of the
+      // 16-bit loads): K to T for the score MFMAs, V to fp16, which holds
+      // every e4m3 value, for the fp16 P.V below.
 #pragma unroll
       for (int i = 0; i < NQK; ++i) R.k[i] = fp8x8_to<T>(R.k8[i]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) R.v[r] = __builtin_bit_cast(vchunk_t, fp8x8_to<T>(R.v8[r]));
+      for (int r = 0; r < 4; ++r)
+        R.v[r] = __builtin_bit_cast(vchunk_t, fp8x8_to<_Float16>(R.v8[r]));
     }
     if constexpr (KT) {
       // R.k[i] holds row 4j + i, bytes 16 n16 .. +16 (the V pattern). Through
@@ -321,20 +323,34 @@ struct DecodeWave {
       }
     }
 
-    const pv_t pa = pack4<T>(pf);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) lo[r] = pf[r] - (float)pa[r];
-    const pv_t pl = pack4<T>(lo);
-#pragma unroll
-    for (int m = 0; m < CH; ++m) {
+    // B operand of output block m: element m of the lane's four V rows.
+    auto vcol = [&](int m) -> u32x2 {
       const uint32_t w0 = (m & 1) ? pair_hi(R.v[0][m >> 1], R.v[1][m >> 1])
                                   : pair_lo(R.v[0][m >> 1], R.v[1][m >> 1]);
       const uint32_t w1 = (m & 1) ? pair_hi(R.v[2][m >> 1], R.v[3][m >> 1])
                                   : pair_lo(R.v[2][m >> 1], R.v[3][m >> 1]);
-      const u32x2 w = {w0, w1};
-      const pv_t vb = __builtin_bit_cast(pv_t, w);
-      o[m] = MfV::run(pa, vb, o[m]);
-      o[m] = MfV::run(pl, vb, o[m]);
+      return (u32x2){w0, w1};
+    };
+    if constexpr (KV8) {
+      // fp8 pools: P.V in fp16, one MFMA per block. P lies in [0, 1], where
+      // fp16 keeps 11 significant bits (relative rounding <= 2^-12, below
+      // the rounding of a 16-bit output).
+      typedef Mfma16x16x16<_Float16> MfH;
+      const typename MfH::op_t ph = pack4<_Float16>(pf);
+#pragma unroll
+      for (int m = 0; m < CH; ++m)
+        o[m] = MfH::run(ph, __builtin_bit_cast(typename MfH::op_t, vcol(m)), o[m]);
+    } else {
+      const pv_t pa = pack4<T>(pf);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lo[r] = pf[r] - (float)pa[r];
+      const pv_t pl = pack4<T>(lo);
+#pragma unroll
+      for (int m = 0; m < CH; ++m) {
+        const pv_t vb = __builtin_bit_cast(pv_t, vcol(m));
+        o[m] = MfV::run(pa, vb, o[m]);
+        o[m] = MfV::run(pl, vb, o[m]);
+      }
     }
   }
 

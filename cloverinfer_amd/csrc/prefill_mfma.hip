@@ -49,7 +49,8 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRT = 2;                  // 16-row MFMA tiles per wave
-constexpr int kRows = kWaves * kRT * 16; // query rows per workgroup
+constexpr int kWaveRows = kRT * 16;     // query rows per wave
+constexpr int kRows = kWaves * kWaveRows; // query rows per workgroup
 constexpr int kBK = 64;                 // K/V tokens per tile
 constexpr float kRescaleLog2 = 8.f;     // lazy-rescale threshold (log2 units)
 
@@ -153,12 +154,12 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   const float c = fmaxf(fabsf(p.scale_log2), 0x1p-126f);
   const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
 
-  // Q (B operand of S^T = K Q^T) for this lane's rows 32w + 16rt + n16.
+  // Q (B operand of S^T = K Q^T) for this lane's rows kWaveRows*w + 16rt + n16.
   u32x4 qop[kRT][NQK];  // kept as raw words: bit-cast to the operand type at each MFMA
   int lim[kRT];  // last visible position of the lane's softmax row (-1: no row)
 #pragma unroll
   for (int rt = 0; rt < kRT; ++rt) {
-    const int r = 32 * wave + 16 * rt + n16;
+    const int r = kWaveRows * wave + 16 * rt + n16;
     const int tok = q0 + r / G;
     const bool ok = r < bq * G && tok < n_new;
     lim[rt] = ok ? base_pos + tok : -1;
@@ -174,7 +175,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   }
   // Smallest causal limit over the wave's real rows (rows are ordered by
   // token): tiles ending at or below it need no causal mask.
-  const int wave_row0 = 32 * wave;
+  const int wave_row0 = kWaveRows * wave;
   const int wave_lim = (wave_row0 < bq * G && q0 + wave_row0 / G < n_new)
                            ? base_pos + q0 + wave_row0 / G : -1;
 
@@ -455,13 +456,13 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     if (overflow) run_tiles(std::true_type{});
   }
 
-  // ---- normalise and store rows 32w + 16rt + 4j + e
+  // ---- normalise and store rows kWaveRows*w + 16rt + 4j + e
 #pragma unroll
   for (int rt = 0; rt < kRT; ++rt) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float l = lsum[rt][e];
-      const int row = 32 * wave + 16 * rt + 4 * j + e;
+      const int row = kWaveRows * wave + 16 * rt + 4 * j + e;
       const int tok = q0 + row / G;
       if (row >= bq * G || tok >= n_new) continue;
       const float inv = l > 0.f ? 1.f / l : 0.f;

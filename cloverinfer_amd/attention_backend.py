@@ -26,6 +26,7 @@ from __future__ import annotations
 import math
 from typing import Dict, List, Optional
 
+import numpy as np
 import torch
 
 from . import kernels
@@ -33,13 +34,15 @@ from .block_table import DeviceBlockTable
 
 
 class _Request:
-    __slots__ = ("blocks", "layer_lens", "context_len", "row")
+    __slots__ = ("blocks", "row")
 
-    def __init__(self, blocks: List[int], num_layers: int, seq_len: int, row: int):
-        self.blocks = blocks
-        self.layer_lens = [seq_len] * num_layers
-        self.context_len = seq_len
-        self.row = row  # row of the device block table
+    def __init__(self, blocks: List[int], row: int):
+        self.blocks = blocks  # blocks held, in table order
+        self.row = row        # row of the device block table and of the host state
+
+
+def _align(n: int) -> int:
+    return (n + 255) // 256 * 256
 
 
 # Names accepted for the pool dtype: the resident KV dtype strings of the
@@ -98,6 +101,14 @@ class GpuAttentionBackend:
         self.free_blocks: List[int] = list(range(num_blocks))
         self.requests: Dict[str, _Request] = {}
         self.tables = DeviceBlockTable(self.device)
+        # Host state per table row (so a batch is bookkept with array
+        # operations): tokens held per layer, context length (advanced after
+        # the last layer), blocks held and the row's block-table entries.
+        self._lens = np.zeros((0, 0), dtype=np.int64)
+        self._ctx = np.zeros(0, dtype=np.int64)
+        self._nblk = np.zeros(0, dtype=np.int64)
+        self._htab = np.zeros((0, 0), dtype=np.int64)
+        self._bshift = block_size.bit_length() - 1
         self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
         self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
         self.stats = {"decode_items": 0, "decode_launches": 0, "init_requests": 0}
@@ -154,6 +165,44 @@ class GpuAttentionBackend:
         bs = self.block_size
         return req.blocks[pos // bs] * bs + pos % bs
 
+    def _host_row(self, req: _Request, seq_len: int) -> None:
+        """(Re)initialise the host state of the request's row."""
+        row, nb = req.row, len(req.blocks)
+        rows = max(self._lens.shape[0], 1)
+        while rows <= row:
+            rows *= 2
+        width = max(self._htab.shape[1], 1)
+        while width < nb:
+            width *= 2
+        if rows > self._lens.shape[0] or self.num_layers > self._lens.shape[1]:
+            lens = np.zeros((rows, self.num_layers), dtype=np.int64)
+            lens[:self._lens.shape[0], :self._lens.shape[1]] = self._lens
+            self._lens = lens
+            self._ctx = np.concatenate([self._ctx, np.zeros(rows - self._ctx.size, np.int64)])
+            self._nblk = np.concatenate([self._nblk, np.zeros(rows - self._nblk.size, np.int64)])
+        if rows > self._htab.shape[0] or width > self._htab.shape[1]:
+            tab = np.full((rows, width), -1, dtype=np.int64)
+            tab[:self._htab.shape[0], :self._htab.shape[1]] = self._htab
+            self._htab = tab
+        self._lens[row] = seq_len
+        self._ctx[row] = seq_len
+        self._nblk[row] = nb
+        self._htab[row] = -1
+        self._htab[row, :nb] = req.blocks
+
+    def _grow_request(self, req: _Request) -> None:
+        """One more block for a request whose blocks are full."""
+        blk = self._take_blocks(1, "OOM during append")[0]
+        col = len(req.blocks)
+        self.tables.set(req.row, col, blk)
+        req.blocks.append(blk)
+        if col >= self._htab.shape[1]:
+            tab = np.full((self._htab.shape[0], 2 * self._htab.shape[1]), -1, dtype=np.int64)
+            tab[:, :self._htab.shape[1]] = self._htab
+            self._htab = tab
+        self._htab[req.row, col] = blk
+        self._nblk[req.row] = col + 1
+
     # ------------------------------------------------------------ protocol
     def init_request(self, request_id: str, initial_kv: List[Dict[str, torch.Tensor]],
                      decode_reserve_tokens: int = 0) -> int:
@@ -167,7 +216,7 @@ class GpuAttentionBackend:
         reserve = max(1, int(decode_reserve_tokens))
         nblocks = max(1, math.ceil((seq_len + reserve) / self.block_size))
         blocks = self._take_blocks(nblocks, "OOM: Not enough blocks")
-        req = _Request(blocks, self.num_layers, seq_len, self.tables.add(blocks))
+        req = _Request(blocks, self.tables.add(blocks))
         if seq_len:
             slots = torch.tensor([self._slot(req, p) for p in range(seq_len)],
                                  dtype=torch.int64).to(self.device)
@@ -179,6 +228,7 @@ class GpuAttentionBackend:
                     self.tables.remove(req.row)
                     raise ValueError(f"layer {layer}: key/value shape differs from layer 0")
                 self._append(k, v, layer, slots)
+        self._host_row(req, seq_len)
         self.requests[request_id] = req
         self.stats["init_requests"] += 1
         return seq_len
@@ -229,7 +279,7 @@ class GpuAttentionBackend:
         reserve = max(1, int(decode_reserve_tokens))
         nblocks = max(1, math.ceil((T + reserve) / self.block_size))
         blocks = self._take_blocks(nblocks, "OOM: Not enough blocks")
-        req = _Request(blocks, self.num_layers, T, self.tables.add(blocks))
+        req = _Request(blocks, self.tables.add(blocks))
         if T:
             bs = self.block_size
             pos = torch.arange(T)
@@ -247,6 +297,7 @@ class GpuAttentionBackend:
                 if v.stride(2) != 1:
                     v = v.contiguous()
                 self._append(k, v, layer, slots)
+        self._host_row(req, T)
         self.requests[request_id] = req
         self.stats["init_requests"] += 1
         return T
@@ -262,24 +313,39 @@ class GpuAttentionBackend:
     def decode_layer_batch(self, items: List[Dict[str, object]]) -> List[torch.Tensor]:
         """Items in order; consecutive items of one (layer, scale) with distinct
         requests form one launch pair (append + decode)."""
+        requests = self.requests
+        if items:
+            # The node's batch: one layer and scale, distinct known requests,
+            # checked with a few comprehensions instead of a loop per item.
+            layers = {it["layer_idx"] for it in items}
+            scales = {it.get("score_scale", 1.0) for it in items}
+            if len(layers) == 1 and len(scales) == 1:
+                reqs = [requests.get(it["request_id"]) for it in items]
+                if None not in reqs and len({r.row for r in reqs}) == len(reqs):
+                    return self._run_wave(list(items), reqs, int(layers.pop()),
+                                          float(scales.pop()))
         out: List[torch.Tensor] = []
         wave: List[Dict[str, object]] = []
+        reqs = []
         in_wave = set()
         key = None
         for it in items:
-            rid = str(it["request_id"])
-            if rid not in self.requests:
-                raise KeyError(f"Unknown request {rid}")
+            rid = it["request_id"]
+            req = requests.get(rid)
+            if req is None:
+                req = requests.get(str(rid))
+                if req is None:
+                    raise KeyError(f"Unknown request {rid}")
             k = (int(it["layer_idx"]), float(it.get("score_scale", 1.0)))
-            if wave and (k != key or rid in in_wave):
-                out.extend(self._run_wave(wave, *key))
-                wave = []
-                in_wave = set()
+            if wave and (k != key or req.row in in_wave):
+                out.extend(self._run_wave(wave, reqs, *key))
+                wave, reqs, in_wave = [], [], set()
             key = k
             wave.append(it)
-            in_wave.add(rid)
+            reqs.append(req)
+            in_wave.add(req.row)
         if wave:
-            out.extend(self._run_wave(wave, *key))
+            out.extend(self._run_wave(wave, reqs, *key))
         return out
 
     def _staging(self, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
@@ -294,110 +360,126 @@ class GpuAttentionBackend:
             self._stage[name] = buf
         return buf[:n].view(*shape)
 
-    def _rows(self, items: List[Dict[str, object]], name: str, heads: int, d: int,
-              dt: torch.dtype) -> torch.Tensor:
-        """The items' ``name`` tensors ([heads, d] or [1, heads, d]) as one
-        device tensor [B, heads, d], through one copy."""
-        ts = [it[name] for it in items]
+    def _fill(self, ts: List[torch.Tensor], heads: int, d: int, dt: torch.dtype,
+              raw: torch.Tensor):
+        """The tensors ``ts`` ([heads, d] or [1, heads, d] each) as rows of
+        [B, heads, d]: written into the pinned bytes ``raw`` (returns None; the
+        caller uploads them with the rest), or, when they are already on the
+        device, stacked there (returns that tensor)."""
         n = len(ts)
         t0 = ts[0]
+        host = raw.view(dt).view(n, heads, d)
         if t0.device.type == "cpu" and t0.numel() == heads * d:
             # The node's case (host tensors of one shape): one stack straight
-            # into the pinned buffer; torch checks shapes and devices itself
-            # (and converts dtypes), anything else takes the general path.
-            host = self._staging(name, (n, heads, d), dt)
+            # into the pinned buffer; torch checks shapes and devices (and
+            # converts dtypes), anything else takes the general path.
             try:
                 torch.stack(ts, out=host.view(n, *t0.shape))
-                return host.to(self.device, non_blocking=True)
+                return None
             except (RuntimeError, TypeError):
                 pass
-        shape = t0.shape
-        same = all(t.shape == shape for t in ts) and t0.numel() == heads * d
-        if same and all(t.device == self.device for t in ts):
+        idx = self.device.index
+        if t0.numel() == heads * d and all(
+                t.shape == t0.shape and t.is_cuda and (idx is None or t.get_device() == idx)
+                for t in ts):
             return torch.stack(ts).view(n, heads, d).to(dt)
-        host = self._staging(name, (n, heads, d), dt)
-        if same and all(t.dtype == dt and t.device.type == "cpu" for t in ts):
-            torch.stack(ts, out=host.view(n, *shape))
-        else:
-            host.copy_(torch.stack([t.reshape(heads, d).to("cpu") for t in ts]))
-        return host.to(self.device, non_blocking=True)
+        host.copy_(torch.stack([t.reshape(heads, d).to("cpu") for t in ts]))
+        return None
 
-    def _run_wave(self, items: List[Dict[str, object]], layer: int,
+    def _run_wave(self, items: List[Dict[str, object]], reqs: List[_Request], layer: int,
                   score_scale: float) -> List[torch.Tensor]:
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"layer_idx {layer} outside [0, {self.num_layers})")
         _, _, bs, hkv, d = self.k_pools.shape
         if self._stage_done is not None:
-            self._stage_done.synchronize()  # the staging buffers are free again
-        q0 = items[0]["query"]
-        hq = q0.numel() // d
+            self._stage_done.synchronize()  # the staging buffer is free again
         n = len(items)
+        qs = [it["query"] for it in items]
+        ks = [it["key"] for it in items]
+        vs = [it["value"] for it in items]
+        q0 = qs[0]
+        hq = q0.numel() // d
         dt = self._compute_dtype(q0.dtype)
-        q = self._rows(items, "query", hq, d, dt)
-        kdt = self._append_dtype(items[0]["key"].dtype)  # fp8 pools: quantised once, from the payload
-        k = self._rows(items, "key", hkv, d, kdt)
-        v = self._rows(items, "value", hkv, d, kdt)
+        kdt = self._append_dtype(ks[0].dtype)  # fp8 pools: quantised once, from the payload
 
-        # Metadata, one copy: slots (int64), new block-table entries (int64
-        # rows / columns / blocks), context lengths and table rows (int32).
-        reqs = [self.requests[str(it["request_id"])] for it in items]
-        slots, lens, rows = [], [], []
-        for req in reqs:
-            pos = req.layer_lens[layer]
-            if pos >= len(req.blocks) * bs:
-                blk = self._take_blocks(1, "OOM during append")[0]
-                self.tables.set(req.row, len(req.blocks), blk)
-                req.blocks.append(blk)
-            slots.append(req.blocks[pos // bs] * bs + pos % bs)
-            req.layer_lens[layer] = pos + 1
-            lens.append(pos + 1)
-            rows.append(req.row)
+        # Bookkeeping over the requests' rows: the new token of request i
+        # goes to position pos[i] of this layer (a request whose blocks are
+        # full takes one more first).
+        rows = np.fromiter((r.row for r in reqs), dtype=np.int64, count=n)
+        pos = self._lens[rows, layer]
+        for i in np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist():
+            self._grow_request(reqs[i])
+        slots = self._htab[rows, pos >> self._bshift] * bs + (pos & (bs - 1))
+        lens = pos + 1
+        self._lens[rows, layer] = lens
         upd = self.tables.take_pending()
         nu = len(upd)
-        meta = self._staging("meta", (4 * n + 6 * nu,), torch.int32)
-        wide = [*slots]
-        for part in range(3):
-            wide.extend(u[part] for u in upd)
-        meta[:2 * (n + 3 * nu)].view(torch.int64).copy_(torch.tensor(wide, dtype=torch.int64))
-        meta[2 * (n + 3 * nu):].copy_(torch.tensor(lens + rows, dtype=torch.int32))
-        meta_dev = meta.to(self.device, non_blocking=True)
+
+        # One pinned buffer, one upload: q | k | v | int64 slots and table
+        # updates (rows, columns, blocks) | int32 context lengths and rows.
+        qb = n * hq * d * torch.finfo(dt).bits // 8
+        kb = n * hkv * d * torch.finfo(kdt).bits // 8
+        o_k = _align(qb)
+        o_v = o_k + _align(kb)
+        o_w = o_v + _align(kb)
+        o_i = o_w + _align(8 * (n + 3 * nu))
+        total = o_i + 8 * n
+        buf = self._staging("wave", (total,), torch.uint8)
+        q = self._fill(qs, hq, d, dt, buf[:qb])
+        k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
+        v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
+        wide = buf[o_w:o_w + 8 * (n + 3 * nu)].numpy().view(np.int64)
+        wide[:n] = slots
+        if nu:
+            wide[n:] = np.asarray(upd, dtype=np.int64).T.reshape(-1)
+        narrow = buf[o_i:total].numpy().view(np.int32)
+        narrow[:n] = lens
+        narrow[n:] = rows
+        dev = buf.to(self.device, non_blocking=True)
         self._stage_done = torch.cuda.Event()
         self._stage_done.record()
-        wide_dev = meta_dev[:2 * (n + 3 * nu)].view(torch.int64)
+        if q is None:
+            q = dev[:qb].view(dt).view(n, hq, d)
+        if k is None:
+            k = dev[o_k:o_k + kb].view(kdt).view(n, hkv, d)
+        if v is None:
+            v = dev[o_v:o_v + kb].view(kdt).view(n, hkv, d)
+        wide_dev = dev[o_w:o_w + 8 * (n + 3 * nu)].view(torch.int64)
         if nu:
             self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
         slots_dev = wide_dev[:n]
-        ctx_dev = meta_dev[2 * (n + 3 * nu):2 * (n + 3 * nu) + n]
-        bt = self.tables.rows(rows, meta_dev[2 * (n + 3 * nu) + n:])
+        narrow_dev = dev[o_i:total].view(torch.int32)
+        ctx_dev = narrow_dev[:n]
+        bt = self.tables.rows(rows.tolist(), narrow_dev[n:])
         ctx_out = torch.empty_like(q)
         kp, vp = self.k_pools[layer], self.v_pools[layer]
+        max_len = int(lens.max())
         if self.partition_size is None and kernels.append_fusable(q, kp, n):
             # Append and decode in one call: the new rows land at position
             # lens - 1, the slots computed above.
-            kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens), k, v,
+            kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len, k, v,
                                            scale=score_scale)
         else:
             self._append(k, v, layer, slots_dev)
-            kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max(lens),
+            kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
                                     scale=score_scale, partition_size=self.partition_size,
                                     k_scale=self.k_scales, v_scale=self.v_scales)
         if layer == self.num_layers - 1:
-            for req in reqs:
-                req.context_len += 1
+            self._ctx[rows] += 1
         self.stats["decode_items"] += n
         self.stats["decode_launches"] += 1
         # Outputs in each query's dtype and on its device: one copy for the
         # batch when the queries agree (the node's case), per item otherwise.
-        want = {(it["query"].device, it["query"].dtype) for it in items}
-        if len(want) == 1:
-            dev, qdt = want.pop()
-            res = ctx_out.to(device=dev, dtype=qdt)
-            return list(res.split(1))
-        return [ctx_out[i:i + 1].to(device=it["query"].device, dtype=it["query"].dtype)
-                for i, it in enumerate(items)]
+        qdt, qdev = q0.dtype, q0.device
+        if all(t.dtype == qdt for t in qs) and (
+                (qdev.type == "cpu" and all(not t.is_cuda for t in qs))
+                or all(t.device == qdev for t in qs)):
+            res = ctx_out.to(device=qdev, dtype=qdt)
+            return list(res.view(n, 1, hq, d).unbind(0))
+        return [ctx_out[i:i + 1].to(device=t.device, dtype=t.dtype) for i, t in enumerate(qs)]
 
     def get_context_len(self, request_id: str) -> int:
-        return self.requests[request_id].context_len
+        return int(self._ctx[self.requests[request_id].row])
 
     def free_request(self, request_id: str) -> None:
         req = self.requests.pop(request_id, None)

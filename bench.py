@@ -187,8 +187,15 @@ def bench_decode(args, cfg):
     w = decode_workload(cfg, dev)
     out = torch.empty_like(w["q"])
     max_ctx = max(w["ctx"])
-    a = kernels.decode_args(out, w["q"], w["k"], w["v"], w["table"], w["ctx_dev"], w["bs"],
-                            max_ctx, scale=w["scale"])
+    # A pool smaller than 512 MiB would be served from the 256 MB Infinity
+    # Cache after the first step: such workloads rotate over enough copies of
+    # the pools to stream at least 512 MiB between two visits of one copy.
+    pool_bytes = 2 * w["k"].numel() * w["k"].element_size()
+    copies = max(1, math.ceil((512 << 20) / pool_bytes))
+    pools = [(w["k"], w["v"])] + [(w["k"].clone(), w["v"].clone()) for _ in range(copies - 1)]
+    args_list = [kernels.decode_args(out, w["q"], kc, vc, w["table"], w["ctx_dev"], w["bs"],
+                                     max_ctx, scale=w["scale"]) for kc, vc in pools]
+    a = args_list[0]
     part = args.partition if args.partition is not None else cfg["partition"]
     if part is not None and part < 0:  # explicit request for the automatic schedule
         part = None
@@ -212,7 +219,8 @@ def bench_decode(args, cfg):
     else:
         ws = None
 
-    def first_half():
+    def first_half(i=0):
+        a = args_list[i % copies]
         if mode == "balanced":
             kernels.balanced_partials(a, waves, ws, stream.cuda_stream)
         elif mode == "split":
@@ -220,24 +228,26 @@ def bench_decode(args, cfg):
         else:
             kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
 
-    def second_half():
+    def second_half(i=0):
+        a = args_list[i % copies]
         if mode == "balanced":
             kernels.balanced_reduce(a, waves, ws, stream.cuda_stream)
         elif mode == "split":
             kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
 
-    def step():
-        first_half()
-        second_half()
+    def step(i=0):
+        first_half(i)
+        second_half(i)
 
-    log(f"warmup {args.warmup} (mode {mode}, partition {part if mode == 'split' else 0})")
-    for _ in range(args.warmup):
-        step()
+    log(f"warmup {args.warmup} (mode {mode}, partition {part if mode == 'split' else 0}, "
+        f"{copies} pool copies)")
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        step(args.warmup + i)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = wall / args.steps * 1e3
@@ -247,11 +257,11 @@ def bench_decode(args, cfg):
     # queued, so host launch gaps stay out of the event intervals.
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     torch.cuda._sleep(50_000_000)
-    for e in ev:
+    for i, e in enumerate(ev):
         e[0].record(stream)
-        first_half()
+        first_half(i)
         e[1].record(stream)
-        second_half()
+        second_half(i)
         e[2].record(stream)
     torch.cuda.synchronize()
     dec_us, dec_med = _event_us(ev, 0, 1)
@@ -289,6 +299,7 @@ def bench_decode(args, cfg):
             "max_context_len": max_ctx,
             "schedule": mode,
             "partition_size": part if mode == "split" else 0,
+            "kv_pool_copies": copies,
             "algorithmic_bytes_per_step": w["algo_bytes"],
             "seed": cfg["seed"],
         },

@@ -34,6 +34,11 @@
 // P stays below 2^8. Tiles fully below every row's causal limit, with all
 // block-table entries valid, skip the per-element masks.
 //
+// Inside each MFMA phase the LDS operand reads run ahead of the MFMAs that
+// use them (K: one k-step ahead; V: three output blocks ahead), held in that
+// order by scheduling barriers; left alone, the compiler issues them just
+// before their MFMAs and the wave waits out the LDS latency at every pair.
+//
 // K/V tiles go through a three-stage LDS ring: the global loads of tile k+1
 // are in flight while tile k is computed, and the P.V of the last half-step
 // of tile k - 1 still reads its V; block-table entries are fetched one tile
@@ -277,19 +282,37 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     auto qk = [&](int g) {
       const T *K = sK[(g >> 1) % 3];
       const int half = g & 1;
+      // K operands of k-step i + 1 are read while the MFMAs of k-step i run
+      // (the scheduling barriers keep the compiler from sinking the reads).
+      auto kread = [&](int h, int i) {
+        return load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * KROW + 32 * i + 8 * j]);
+      };
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) sacc[h][rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      u32x4 cur[2] = {kread(0, 0), kread(1, 0)};
 #pragma unroll
-        for (int i = 0; i < NQK; ++i) {
-          const qk_t a = __builtin_bit_cast(
-              qk_t, load_vec<u32x4>(&K[(32 * half + 16 * h + n16) * KROW + 32 * i + 8 * j]));
+      for (int i = 0; i < NQK; ++i) {
+        u32x4 nxt[2];
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < NQK) {
+          nxt[0] = kread(0, i + 1);
+          nxt[1] = kread(1, i + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int rt = 0; rt < kRT; ++rt)
-            sacc[h][rt] = MfQK::run(a, __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
+            sacc[h][rt] = MfQK::run(__builtin_bit_cast(qk_t, cur[h]),
+                                    __builtin_bit_cast(qk_t, qop[rt][i]), sacc[h][rt]);
+        if (i + 1 < NQK) {
+          cur[0] = nxt[0];
+          cur[1] = nxt[1];
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     };
     // O += P V for step g. B operand of MFMA m (output columns 16m + n16):
     // lane (n16, j) needs V[token of k-slot 4h + kk][16m + n16], two
@@ -298,6 +321,16 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
         p_t, (u32x4){EXACT ? 0x3f803f80u : 0x3c003c00u, EXACT ? 0x3f803f80u : 0x3c003c00u,
                      EXACT ? 0x3f803f80u : 0x3c003c00u, EXACT ? 0x3f803f80u : 0x3c003c00u});
     auto pv = [&](int g) {
+      const uint16_t *vrow = &sV[(g >> 1) % 3][(32 * (g & 1) + 4 * j + (n16 >> 2)) * VROW +
+                                               4 * (n16 & 3)];
+      auto vread = [&](int m) { return vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m); };
+      // V operands go out PVD blocks ahead of their MFMAs (a rolling window,
+      // kept in order by the scheduling barriers).
+      constexpr int PVD = 3;
+      u32x4 vq[PVD];
+#pragma unroll
+      for (int m = 0; m < PVD; ++m) vq[m] = vread(m);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int rt = 0; rt < kRT; ++rt) {
         if constexpr (!EXACT) {
@@ -307,12 +340,12 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
           lsum[rt] = MfB::run(pl[rt], ones, lsum[rt]);
         }
       }
-      const uint16_t *vrow = &sV[(g >> 1) % 3][(32 * (g & 1) + 4 * j + (n16 >> 2)) * VROW +
-                                               4 * (n16 & 3)];
 #pragma unroll
       for (int m = 0; m < CH; ++m) {
-        const p_t vb =
-            __builtin_bit_cast(p_t, vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m));
+        const p_t vb = __builtin_bit_cast(p_t, vq[m % PVD]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (m + PVD < CH) vq[m % PVD] = vread(m + PVD);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
           if constexpr (!EXACT) {
@@ -323,6 +356,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
           }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     };
     // Scores of step g that a row may not see (unreadable block, past the
     // row's causal limit) become -inf: they drop out of the row max and, as

@@ -452,10 +452,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     bool full_prev = false;
     for (int tile = 0; tile < ntiles; ++tile) {
       const bool more = tile + 1 < ntiles;
-      if (more) {
-        load_tile(tile + 1);     // block ids fetched last iteration
-        fetch_blocks(tile + 2);  // block-table entries for the tile after
-      }
+      if (more) load_tile(tile + 1);  // block ids fetched last iteration
       const bool full = tile_full(tile);
       const int g = 2 * tile;
       // The MFMA phases run at raised wave priority: the SIMD's arbiter then
@@ -466,6 +463,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       qk(g);
       if (tile > 0) pv(g - 1);
       __builtin_amdgcn_s_setprio(0);
+      // Block-table entries for the tile after next, issued before a softmax
+      // (VALU only on full tiles): the scalar loads share the LDS wait
+      // counter, so issued right before an LDS read they would be waited for
+      // there.
+      if (more) fetch_blocks(tile + 2);
       softmax_step(g, full);
       __builtin_amdgcn_s_setprio(1);
       qk(g + 1);

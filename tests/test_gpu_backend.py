@@ -191,3 +191,48 @@ def test_resident_kv_dtype_knob(knob):
                                        "value": rnd(it["value"])}])[0]
         assert got.dtype == torch.float32
         assert_attention_close(got, ref, what=f"layer {layer}")
+
+
+def test_many_requests_long_rows_mixed_batches():
+    """More requests than the initial table rows (64) and rows wider than its
+    initial width (64 blocks), so the device table and the host state grow;
+    batches that mix layers and repeat a request (split into several
+    launches, in order); payloads on the device in some steps."""
+    g = torch.Generator().manual_seed(41)
+    hq, hkv, d, dtype, layers = 8, 2, 64, torch.float16, 2
+    gpu = GpuAttentionBackend(num_blocks=4096, block_size=16)
+    cpu = CpuAttentionOracle()
+    lens = [int(x) for x in torch.randint(0, 120, (80,), generator=g)]
+    lens[3], lens[70] = 1100, 1023  # 69 and 64 blocks: past the initial width
+    rids = [f"m{i}" for i in range(len(lens))]
+    for rid, T in zip(rids, lens):
+        kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(T, hkv, d, generator=g).to(dtype)} for _ in range(layers)]
+        assert gpu.init_request(rid, kv) == cpu.init_request(rid, kv) == T
+
+    def item(rid, layer, dev):
+        return {"request_id": rid, "layer_idx": layer,
+                "query": torch.randn(1, hq, d, generator=g).to(dtype).to(dev),
+                "key": torch.randn(1, hkv, d, generator=g).to(dtype).to(dev),
+                "value": torch.randn(1, hkv, d, generator=g).to(dtype).to(dev),
+                "score_scale": d ** -0.5}
+
+    for step in range(18):
+        dev = "cuda" if step % 4 == 1 else "cpu"
+        if step % 3 == 2:
+            # one call: layer 0 for all, a request repeated, then layer 1 for all
+            items = [item(r, 0, dev) for r in rids] + [item(rids[5], 1, dev), item(rids[5], 1, dev)]
+            items += [item(r, 1, dev) for r in rids if r != rids[5]]
+            calls = [items]
+        else:
+            calls = [[item(r, layer, dev) for r in rids] for layer in range(layers)]
+        for items in calls:
+            got = gpu.decode_layer_batch(items)
+            ref = cpu.decode_layer_batch([{k: (v.cpu() if torch.is_tensor(v) else v)
+                                           for k, v in it.items()} for it in items])
+            for a, b in zip(got, ref):
+                assert a.device.type == dev.split(":")[0]
+                assert_attention_close(a.cpu(), b, what=f"step {step}")
+    for rid in rids:
+        assert gpu.get_context_len(rid) == cpu.get_context_len(rid)
+    assert gpu.tables.table.shape[0] >= 80 and gpu.tables.width >= 70

@@ -47,7 +47,6 @@ from __future__ import annotations
 
 import argparse
 import io
-import math
 import struct
 import sys
 import time
@@ -231,8 +230,9 @@ class KVSlotServer:
     def request(self, payload: bytes) -> bytes:
         """Answers every message in ``payload``; raises KVSlotProtocolError
         on the first invalid one."""
-        fin, reader, out = io.BytesIO(payload), None, []
+        fin = io.BytesIO(payload)
         reader = _Reader(fin)
+        out = []
         while fin.tell() < len(payload):
             out.append(self.handle(reader.read(HEADER.size, "kvslot header"), reader))
         return b"".join(out)

@@ -45,6 +45,13 @@ DECODE_CONFIGS = {
                    vscale=1.0, seed=1003, partition=None,
                    workload="paged decode, GQA Qwen2.5-7B shape: 128 seqs, 28 q / 4 kv heads, "
                             "head_dim 128, block 16, bf16, context U[256,8192] seeded per sequence"),
+    # The same batch over fp32 pools: the reference's default resident KV
+    # dtype and what its CPU dense nodes hand over (src/core/nodes.py:21-24).
+    "qwen7b_fp32": dict(num_seqs=128, hq=28, hkv=4, d=128, dtype="float32",
+                        ctx=("uniform", 256, 8192), vscale=1.0, seed=1003, partition=None,
+                        workload="paged decode, GQA Qwen2.5-7B shape over fp32 pools: 128 seqs, "
+                                 "28 q / 4 kv heads, head_dim 128, block 16, fp32, context "
+                                 "U[256,8192] seeded per sequence"),
     "long32k": dict(num_seqs=16, hq=32, hkv=8, d=128, dtype="float16", ctx=("fixed", 32768),
                     vscale=1.0, seed=1004, partition=512,
                     workload="split-K paged decode: 16 seqs, 32 q / 8 kv heads, head_dim 128, "

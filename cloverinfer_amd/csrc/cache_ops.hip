@@ -191,15 +191,16 @@ hipError_t launch_reshape_and_cache_fp8(const CacheParams &p, int src_dtype, con
   return hipSuccess;
 }
 
-hipError_t launch_append_by_table(const DecodeParams &p, hipStream_t stream) {
-  // Validated by the caller: 16-byte aligned pointers and strides, 16-bit
-  // elements, rows of head_dim * 2 bytes.
-  const int chunks = p.head_dim * 2 / 16;
+hipError_t launch_append_by_table(const DecodeParams &p, int elem_bytes, hipStream_t stream) {
+  // Validated by the caller: 16-byte aligned pointers and strides, rows of
+  // head_dim * elem_bytes bytes (a multiple of 16).
+  const int chunks = p.head_dim * elem_bytes / 16;
   const int64_t work = (int64_t)p.num_seqs * p.num_kv_heads * chunks;
   if (work == 0) return hipSuccess;
   if (work >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
   const unsigned blocks = (unsigned)((work + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(append_by_table_vec16, dim3(blocks), dim3(kThreads), 0, stream, p, chunks, 2);
+  hipLaunchKernelGGL(append_by_table_vec16, dim3(blocks), dim3(kThreads), 0, stream, p, chunks,
+                     elem_bytes);
   return hipGetLastError();
 }
 

@@ -348,7 +348,8 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   const size_t rows = ((size_t)num_waves + (size_t)nseg) * 16;
   char *ws = (char *)workspace;
   p->num_waves = num_waves;
-  p->stream_depth = stream_depth_setting();
+  // fp32 steps are twice the bytes: two steps in flight (a sweep over 2-4).
+  p->stream_depth = stream_depth_setting(a->dtype == CLV_F32 ? 2 : 3);
   p->stream_run_cost = stream_run_cost_setting();
   p->num_segments = (int32_t)nseg;
   p->seg_prefix = (int32_t *)ws;
@@ -407,9 +408,9 @@ int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const
   p.new_stride_seq = new_stride_seq;
   p.new_stride_head = new_stride_head;
   const hipStream_t s = (hipStream_t)stream;
-  if (clv::stream_appends_in_kernel(a->head_dim, a->block_size, p.group)) {
+  if (clv::stream_appends_in_kernel((DType)a->dtype, a->head_dim, a->block_size, p.group)) {
     p.append_new = 1;
-  } else if (clv::launch_append_by_table(p, s) != hipSuccess) {
+  } else if (clv::launch_append_by_table(p, eb, s) != hipSuccess) {
     return CLV_ELAUNCH;
   }
   if (clv::launch_decode_stream(p, (DType)a->dtype, s) != hipSuccess) return CLV_ELAUNCH;

@@ -101,7 +101,7 @@ hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t str
 // Writes key_new/value_new[s] at position context_lens[s] - 1 of every
 // sequence (slot from its block table), for the decode shapes whose stream
 // kernel does not append itself.
-hipError_t launch_append_by_table(const DecodeParams &p, hipStream_t stream);
+hipError_t launch_append_by_table(const DecodeParams &p, int elem_bytes, hipStream_t stream);
 // KV append into fp8 (OCP e4m3) pools: cache = e4m3(clamp(x / scale[h], +-448)),
 // rounded to nearest even; key/value in CacheParams' elem_bytes (2 or 4).
 hipError_t launch_reshape_and_cache_fp8(const CacheParams &p, int src_dtype, const float *k_scales,
@@ -113,7 +113,7 @@ bool decode_mfma_supported(DType dt, int head_dim, int block_size);
 bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments);
 // Whether the stream kernel writes the appended token itself (fused append)
 // for this shape; otherwise launch_append_by_table runs first.
-bool stream_appends_in_kernel(int head_dim, int block_size, int group);
+bool stream_appends_in_kernel(DType dt, int head_dim, int block_size, int group);
 bool prefill_mfma_supported(DType dt, int head_dim, int block_size);
 
 }  // namespace clv

@@ -386,6 +386,228 @@ struct DecodeWave {
   }
 };
 
+// fp32 pools: the per-wave decode of DecodeWave on v_mfma_f32_16x16x4f32
+// (fp32 operands and accumulation: K, V, Q and P are never rounded, as in
+// CpuAttentionBackend's fp32 einsums). Operand layout of that instruction
+// for lane l (measured on gfx950): A[row l%16][k l/16], B[k l/16][col l%16],
+// C rows 4(l/16) .. +4, col l%16. The fragments are DecodeWave's: the score
+// MFMAs leave S[g = n16][t = 4j + r] in the lane, which is its P operand
+// (k = j <-> token 4j + c for MFMA c) of the P.V MFMAs. The order of the
+// score sum over d and the placement of output columns are free, and are
+// chosen so that each load instruction reads contiguous runs: score MFMA
+// c = 4i + e takes d = 16i + 4j + e in lane group j (load i of a K row reads
+// 64 consecutive bytes across the four lane groups; the lane holds the same
+// Q floats), and o[4w + e] holds O[g = 4j + r][d = 64w + 4 n16 + e] (load w
+// of a V row reads 256 consecutive bytes across the 16 lanes of a group).
+template <int D, bool UNI>
+struct DecodeWaveF32 {
+  typedef u32x4 qk_t;                 // four fp32 Q values
+  static constexpr int NQK = D / 16;  // Q / K words per lane (D / 4 floats)
+  static constexpr int CH = D / 16;   // V floats per lane per row = P.V output blocks
+  static constexpr int VW = CH / 4;   // V words per lane per row (64 columns apart)
+  static constexpr int EB = 4;
+  static constexpr int STEP = 16;
+  static constexpr int KT_BYTES = 16;  // no transpose buffer
+
+  struct Regs {
+    u32x4 k[NQK];     // K row n16, floats 16i + 4j .. +4
+    u32x4 v[4][VW];   // V rows 4j + c, floats 64w + 4 n16 .. +4
+    bool ok;          // the lane's V rows lie in a readable block
+  };
+
+  int n16, j;
+  int64_t sblk, stok;
+  int bshift, bmask;
+  unsigned nblocks;
+  float scale_log2;
+  uint32_t k_lane;     // byte offset of K row n16, float 4j, inside a step
+  uint32_t v_lane[4];  // byte offsets of V rows 4j + c, float 4 n16
+  f32x4 o[CH];         // O[g = 4j + r][d = 64 (m / 4) + 4 n16 + m % 4]
+  float m_run;         // running max of row g = n16 (log2 domain)
+  float l_run;         // this lane's share of the row sum
+
+  __device__ __forceinline__ void init(const DecodeParams &p) {
+    const int lane = threadIdx.x & 63;
+    n16 = lane & 15;
+    j = lane >> 4;
+    sblk = p.kv_stride_block * EB;
+    stok = p.kv_stride_token * EB;
+    bshift = p.block_shift;
+    bmask = (1 << bshift) - 1;
+    nblocks = (unsigned)p.num_blocks;
+    scale_log2 = p.scale_log2;
+    k_lane = (uint32_t)(n16 * stok + 4 * j * EB);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v_lane[c] = (uint32_t)((4 * j + c) * stok + 4 * n16 * EB);
+    reset();
+  }
+
+  __device__ __forceinline__ void set_k_lds(char *) {}
+
+  __device__ __forceinline__ void reset() {
+#pragma unroll
+    for (int m = 0; m < CH; ++m) o[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    m_run = kNegInf;
+    l_run = 0.f;
+  }
+
+  // Q rows h0 .. h0+ng-1 of sequence s: word i of the lane holds
+  // Q[g = n16][d = 16i + 4j .. +4] (zero for g >= ng; every lane loads, a
+  // row >= ng re-reads row ng - 1).
+  __device__ __forceinline__ void load_q_raw(const DecodeParams &p, int s, int h0, int ng,
+                                             u32x4 (&raw)[NQK]) const {
+    const int row = min(n16, ng - 1);
+    const float *qrow = (const float *)p.q + (int64_t)s * p.q_stride_seq +
+                        (int64_t)(h0 + row) * p.q_stride_head + 4 * j;
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) raw[i] = load_vec<u32x4>(qrow + 16 * i);
+  }
+  __device__ __forceinline__ void mask_q(const u32x4 (&raw)[NQK], int ng, qk_t (&q)[NQK]) const {
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) q[i] = n16 < ng ? raw[i] : (u32x4){0u, 0u, 0u, 0u};
+  }
+
+  // UNI: the loads of the 16-token step at token `tok` of block `blk` (an
+  // unreadable block reads a readable row and is masked when computed).
+  __device__ __forceinline__ void issue_blk(const char *kbase, const char *vbase, int blk, int tok,
+                                            Regs &R) const {
+    const bool ok = (unsigned)blk < nblocks;
+    const int64_t off = ok ? blk * sblk + tok * stok : 0;
+    R.ok = ok;
+    const rsrc_t rk = make_rsrc(kbase + off);
+    const rsrc_t rv = make_rsrc(vbase + off);
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) R.k[i] = buf_load<u32x4, kCacheDefault>(rk, k_lane + 64u * i);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int w = 0; w < VW; ++w) R.v[c][w] = buf_load<u32x4, kCacheStream>(rv, v_lane[c] + 256u * w);
+  }
+
+  // Block sizes below 16: each lane looks up the blocks of its own rows.
+  __device__ __forceinline__ void issue(const SegGeom &g, int base, Regs &R) const {
+    if constexpr (UNI) {
+      issue_blk(g.kbase, g.vbase, scalar_load_i32(g.bt + (base >> bshift)), base & bmask, R);
+    } else {
+      const int tk = base + n16;
+      const int kb = tk < g.t_end ? g.bt[tk >> bshift] : 0;
+      const bool kok = tk < g.t_end && (unsigned)kb < nblocks;
+      const int64_t koff = (kok ? kb * sblk + (tk & bmask) * stok : 0) + 4 * j * EB;
+      const int tv = base + 4 * j;
+      const int vb = tv < g.t_end ? g.bt[tv >> bshift] : 0;
+      const bool vok = tv < g.t_end && (unsigned)vb < nblocks;
+      R.ok = vok;
+      const int64_t voff = (vok ? vb * sblk + (tv & bmask) * stok : 0) + 4 * n16 * EB;
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) R.k[i] = load_vec<u32x4>(g.kbase + koff + 64 * i);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int w = 0; w < VW; ++w)
+          R.v[c][w] = load_vec<u32x4>(g.vbase + voff + c * stok + 256 * w);
+    }
+  }
+
+  __device__ __forceinline__ static f32x4 mfma(uint32_t a, uint32_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(__builtin_bit_cast(float, a),
+                                                __builtin_bit_cast(float, b), c, 0, 0, 0);
+  }
+
+  // Fold the step starting at `base` into (o, m_run, l_run).
+  __device__ __forceinline__ void compute(int base, int t_end, Regs &R, const qk_t (&q)[NQK]) {
+    // Two accumulators (even / odd k-steps) keep consecutive MFMAs independent.
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NQK; ++i) {
+      s0 = mfma(R.k[i][0], q[i][0], s0);
+      s1 = mfma(R.k[i][1], q[i][1], s1);
+      s0 = mfma(R.k[i][2], q[i][2], s0);
+      s1 = mfma(R.k[i][3], q[i][3], s1);
+    }
+    const f32x4 sacc = s0 + s1;
+    const bool full = __all(base + STEP <= t_end && R.ok);
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = full || (R.ok && base + 4 * j + r < t_end);
+      x[r] = ok ? sacc[r] * scale_log2 : kNegInf;
+    }
+    if (!full) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (x[r] == kNegInf) {
+#pragma unroll
+          for (int w = 0; w < VW; ++w) R.v[r][w] = (u32x4){0u, 0u, 0u, 0u};  // NaN/Inf of unused slots
+        }
+    }
+    float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float msub = (m_new == kNegInf) ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - msub);
+    float pf[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pf[r] = fast_exp2(x[r] - msub);
+    l_run = l_run * alpha + ((pf[0] + pf[1]) + (pf[2] + pf[3]));
+    m_run = m_new;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float a = shfl(alpha, 4 * j + r);
+#pragma unroll
+        for (int m = 0; m < CH; ++m) o[m][r] *= a;
+      }
+    }
+    // P.V: MFMA (c, m) takes token 4j + c (k = j) and output column
+    // 64 (m / 4) + 4 n16 + m % 4.
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t a = __builtin_bit_cast(uint32_t, pf[c]);
+#pragma unroll
+      for (int m = 0; m < CH; ++m) o[m] = mfma(a, R.v[c][m >> 2][m & 3], o[m]);
+    }
+  }
+
+  __device__ __forceinline__ void reduce_rowsum() {
+    l_run += shfl_xor(l_run, 16);
+    l_run += shfl_xor(l_run, 32);
+  }
+
+  // As DecodeWave::store_partial, with this wave's output columns.
+  __device__ __forceinline__ void store_partial(float *ws_o, float *ws_m, float *ws_l,
+                                                int64_t row0, int ng) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * j + r;
+      const float l = shfl(l_run, g);
+      const float mrow = shfl(m_run, g);
+      if (g >= ng) continue;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      float *dst = ws_o + (row0 + g) * D + 4 * n16;
+#pragma unroll
+      for (int m = 0; m < CH; m += 4) {
+        const f32x4 v = {o[m][r] * inv, o[m + 1][r] * inv, o[m + 2][r] * inv, o[m + 3][r] * inv};
+        store_vec<f32x4>(dst + 16 * m, v);
+      }
+      if (n16 == 0) {
+        ws_m[row0 + g] = l > 0.f ? mrow * kLn2 : kNegInf;
+        ws_l[row0 + g] = l;
+      }
+    }
+  }
+};
+
+// The per-wave decode type of the balanced stream kernel.
+template <typename T, int D, bool UNI, bool KV8>
+struct StreamWave {
+  typedef DecodeWave<T, D, UNI, UNI && D == 128, KV8> type;
+};
+template <int D, bool UNI>
+struct StreamWave<float, D, UNI, false> {
+  typedef DecodeWaveF32<D, UNI> type;
+};
+
 // Log-sum-exp merge of n partial rows, the rule of the reference's
 // partial-softmax merge (src/core/resident_kv_store.py:2497-2509) over all
 // rows at once:

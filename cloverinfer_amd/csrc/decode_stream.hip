@@ -83,7 +83,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   // Every global pointer is a separate restrict argument: with stores to the
   // workspace inside the main loop, that is what lets the compiler keep the
   // wave-uniform block-table reads scalar loads.
-  typedef DecodeWave<T, D, UNI, UNI && D == 128, KV8> WV;
+  typedef typename StreamWave<T, D, UNI, KV8>::type WV;
   constexpr int CEB = KV8 ? 1 : (int)sizeof(T);
   typedef typename WV::qk_t qk_t;
   __shared__ __attribute__((aligned(16))) char s_kt[kWaves][WV::KT_BYTES];
@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
 template <typename T, int D, int DEPTH>
 hipError_t launch_stream_tdd(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid((unsigned)((p.num_waves + kWaves - 1) / kWaves));
-  if constexpr (D == 128) {
+  if constexpr (D == 128 && sizeof(T) == 2) {
     if (p.kv_fp8) {  // validated: block_size >= 16, no fused append
       if (p.block_shift < 4 || p.append_new) return hipErrorInvalidValue;
       hipLaunchKernelGGL((paged_decode_stream<T, D, true, DEPTH, false, true>), grid, dim3(kThreads),
@@ -318,24 +318,30 @@ hipError_t launch_sreduce_t(const DecodeParams &p, hipStream_t stream) {
 }  // namespace
 
 bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments) {
-  return decode_mfma_supported(dt, head_dim, block_size) && num_segments <= kStreamMaxSegments;
+  // fp32 pools run on the fp32 MFMA wave (DecodeWaveF32).
+  const bool f32 = dt == DType::F32 && (head_dim == 64 || head_dim == 128) && block_size >= 4;
+  return (f32 || decode_mfma_supported(dt, head_dim, block_size)) &&
+         num_segments <= kStreamMaxSegments;
 }
 
-bool stream_appends_in_kernel(int head_dim, int block_size, int group) {
-  // The K-transpose path (a 16-token step inside one block, head_dim 128)
-  // with one query-head chunk per kv head.
-  return head_dim == 128 && block_size >= 16 && group <= 16;
+bool stream_appends_in_kernel(DType dt, int head_dim, int block_size, int group) {
+  // The 16-bit K-transpose path (a 16-token step inside one block, head_dim
+  // 128) with one query-head chunk per kv head.
+  return (dt == DType::F16 || dt == DType::BF16) && head_dim == 128 && block_size >= 16 &&
+         group <= 16;
 }
 
 hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream) {
   if (dt == DType::BF16) return launch_stream_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_stream_t<_Float16>(p, stream);
+  if (dt == DType::F32 && !p.kv_fp8 && !p.append_new) return launch_stream_t<float>(p, stream);
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_stream_reduce(const DecodeParams &p, DType dt, hipStream_t stream) {
   if (dt == DType::BF16) return launch_sreduce_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_sreduce_t<_Float16>(p, stream);
+  if (dt == DType::F32) return launch_sreduce_t<float>(p, stream);
   return hipErrorInvalidValue;
 }
 

@@ -192,8 +192,8 @@ BALANCED_MAX_SEGMENTS = 4096
 def balanced_supported(a: _native.DecodeArgs) -> bool:
     group = a.num_heads // a.num_kv_heads
     nseg = a.num_seqs * a.num_kv_heads * ((group + 15) // 16)
-    return (a.dtype in (_native.CLV_F16, _native.CLV_BF16) and a.head_dim in (64, 128)
-            and a.block_size >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
+    return (a.dtype in (_native.CLV_F16, _native.CLV_BF16, _native.CLV_F32)
+            and a.head_dim in (64, 128) and a.block_size >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
 
 
 def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
@@ -294,7 +294,7 @@ def append_fusable(q: torch.Tensor, k_cache: torch.Tensor, num_seqs: int) -> boo
     """Whether :func:`paged_attention_append` covers this decode shape."""
     hq, hkv, d = q.shape[1], k_cache.shape[2], k_cache.shape[3]
     nseg = num_seqs * hkv * ((hq // hkv + 15) // 16)
-    return (k_cache.dtype in (torch.float16, torch.bfloat16) and d in (64, 128)
+    return (k_cache.dtype in (torch.float16, torch.bfloat16, torch.float32) and d in (64, 128)
             and k_cache.shape[1] >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
 
 

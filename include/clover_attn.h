@@ -180,7 +180,7 @@ int clv_splitk_reduce(const clv_decode_args *args, int32_t partition_size,
                       clv_stream_t stream);
 
 /*
- * Balanced decode for ragged batches (fp16/bf16, head_dim 64 or 128,
+ * Balanced decode for ragged batches (fp32/fp16/bf16, head_dim 64 or 128,
  * num_seqs * num_kv_heads * ceil(group/16) <= 4096): num_waves waves split
  * the batch's flattened 16-token steps evenly, crossing sequence borders;
  * each writes one partial per (sequence, kv head) it touches and a second
@@ -214,9 +214,9 @@ int clv_balanced_reduce(const clv_decode_args *args, int32_t num_waves,
  * context_lens[s] tokens, the new one included. Same result as
  * clv_reshape_and_cache with those slots followed by
  * clv_paged_decode_balanced, and the same shapes and workspace as the latter
- * (CLV_EUNSUPPORTED otherwise). For head_dim 128, block_size >= 16 and at
- * most 16 query heads per kv head, the decode kernel writes the rows itself
- * (no separate append launch). A sequence appends nothing when
+ * (CLV_EUNSUPPORTED otherwise). For 16-bit pools with head_dim 128,
+ * block_size >= 16 and at most 16 query heads per kv head, the decode kernel
+ * writes the rows itself (no separate append launch). A sequence appends nothing when
  * context_lens[s] is outside [1, min(max_context_len,
  * max_blocks_per_seq*block_size)] or the slot's block-table entry is outside
  * [0, num_blocks). k_cache and v_cache are written. No counterpart kernel

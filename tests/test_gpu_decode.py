@@ -62,7 +62,7 @@ def test_decode_block_sizes(bs, dtype):
 
 
 @pytest.mark.parametrize("num_waves", [1, 3, 7, 64, 1000])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_balanced_decode_wave_counts(num_waves, dtype):
     """The balanced decode splits the batch's steps over any number of waves;
     spans cross sequence and kv-head borders and skip empty contexts."""
@@ -73,6 +73,27 @@ def test_balanced_decode_wave_counts(num_waves, dtype):
     ref = oa.paged_decode(q, k, v, tables, ctx, scale)
     assert_attention_close(got, ref, what=f"balanced W={num_waves}")
     assert torch.equal(got[0].float(), torch.zeros(28, 128))
+
+
+@pytest.mark.parametrize("d,bs", [(128, 16), (64, 16), (128, 8), (64, 4)])
+def test_fp32_balanced_decode_is_fp32_exact(d, bs):
+    """fp32 pools on the fp32 MFMA wave: nothing is rounded below fp32, so
+    the result agrees with the float64 brute force to fp32 accuracy (a bar
+    100x tighter than the 16-bit one)."""
+    ctx = [0, 1, 15, 16, 17, 250, 1031]
+    q, k, v, tables, scale = case(d + bs, ctx, 28, 4, d, bs, torch.float32)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=None)
+    for s, c in enumerate(ctx):
+        if c == 0:
+            assert torch.equal(got[s], torch.zeros(28, d))
+            continue
+        kk, vv = oa.gather_context(k, v, tables[s], c)
+        # float64 attention with the h // G grouping (oa.attend's, in float64)
+        qf = q[s].double().view(4, 7, d)
+        w = torch.softmax(torch.einsum("kgd,lkd->kgl", qf, kk.double()) * scale, dim=-1)
+        want = torch.einsum("kgl,lkd->kgd", w, vv.double()).reshape(28, d)
+        err = (got[s].double() - want).abs().max().item()
+        assert err < 2e-5, (s, c, err)
 
 
 def test_balanced_decode_many_segments():

@@ -508,11 +508,13 @@ def bench_copy(args):
                        "bytes_read_per_step": n, "bytes_written_per_step": n}}
 
 
-def bench_node(args):
+def bench_node(args, dtype_name="bfloat16"):
     """The "gpu" AttentionNode backend end to end: one decode_layer_batch of
     the GQA Qwen2.5-7B shape batch (128 requests, 28 q / 4 kv heads, head_dim
-    128, bf16, contexts U[256, 8192]) with the query/key/value rows on the host,
-    as the node receives them; wall time per call, host work included."""
+    128, contexts U[256, 8192]) with the query/key/value rows on the host, as
+    the node receives them; wall time per call, host work included. bf16, or
+    fp32 (what the reference's CPU dense nodes send, src/core/nodes.py:21-24;
+    the pools then default to fp32)."""
     import torch
     from cloverinfer_amd.attention_backend import GpuAttentionBackend
 
@@ -524,15 +526,16 @@ def bench_node(args):
     nb = sum(math.ceil((c + steps_total + 1) / bs) for c in ctx) + 16
     be = GpuAttentionBackend(num_blocks=nb, block_size=bs, device="cuda")
     g = torch.Generator(device=dev).manual_seed(cfg["seed"])
+    dt = getattr(torch, dtype_name)
     for i, c in enumerate(ctx):
-        k = torch.randn((c, hkv, d), generator=g, device=dev).to(torch.bfloat16)
-        v = torch.randn((c, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn((c, hkv, d), generator=g, device=dev).to(dt)
+        v = torch.randn((c, hkv, d), generator=g, device=dev).to(dt)
         be.init_request(f"r{i}", [{"key": k, "value": v}], decode_reserve_tokens=steps_total + 1)
     gh = torch.Generator().manual_seed(cfg["seed"] + 1)
     items = [{"request_id": f"r{i}", "layer_idx": 0,
-              "query": torch.randn((1, hq, d), generator=gh).to(torch.bfloat16),
-              "key": torch.randn((1, hkv, d), generator=gh).to(torch.bfloat16),
-              "value": torch.randn((1, hkv, d), generator=gh).to(torch.bfloat16),
+              "query": torch.randn((1, hq, d), generator=gh).to(dt),
+              "key": torch.randn((1, hkv, d), generator=gh).to(dt),
+              "value": torch.randn((1, hkv, d), generator=gh).to(dt),
               "score_scale": d ** -0.5} for i in range(S)]
     for _ in range(args.warmup):
         be.decode_layer_batch(items)
@@ -545,7 +548,8 @@ def bench_node(args):
     return {"metric": "gpu AttentionNode backend: decode_layer_batch wall time per layer",
             "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-            "dtype": "bf16", "data": "synthetic N(0,1), seeded; q/k/v rows on the host",
+            "dtype": {"bfloat16": "bf16", "float32": "f32"}[dtype_name],
+            "data": "synthetic N(0,1), seeded; q/k/v rows on the host",
             "config": {"workload": "decode_layer_batch of 128 requests, GQA Qwen2.5-7B shape, "
                                    "contexts U[256,8192], one layer, host-side q/k/v"},
             "requests_per_s": S / (ms * 1e-3)}
@@ -559,7 +563,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="qwen7b",
-                    choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node"])
+                    choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node",
+                                                      "node_fp32"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass, -1 or default: automatic)")
     ap.add_argument("--waves", type=int, default=0,
@@ -586,6 +591,8 @@ def main() -> int:
         result = bench_copy(args)
     elif args.config == "node":
         result = bench_node(args)
+    elif args.config == "node_fp32":
+        result = bench_node(args, "float32")
     else:
         result = bench_decode(args, DECODE_CONFIGS[args.config])
     print(json.dumps(result), flush=True)

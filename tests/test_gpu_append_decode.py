@@ -28,6 +28,8 @@ def _same_bits(a, b):
     (32, 1, 128, 16, torch.bfloat16),   # 32 query heads per kv head: append kernel first
     (16, 2, 64, 16, torch.float16),     # head_dim 64: append kernel first
     (14, 2, 128, 8, torch.bfloat16),    # block_size 8: append kernel first
+    (28, 4, 128, 16, torch.float32),    # fp32 pools: append kernel (4-byte rows), fp32 MFMA wave
+    (16, 2, 64, 8, torch.float32),      # idem, head_dim 64, block_size 8
 ])
 def test_fused_append_decode(hq, hkv, d, bs, dtype):
     ctx0 = [1, 15, 16, 31, 100, 0, 47]  # 0: no new token, zero output, pool untouched

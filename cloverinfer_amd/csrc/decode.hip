@@ -66,7 +66,7 @@ __device__ __forceinline__ OutDesc<T> out_desc(const DecodeParams &p, int s, int
 template <typename T, int D, int NW, bool UNI>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
-  typedef DecodeWave<T, D, UNI> W;
+  typedef typename GridWave<T, D, UNI>::type W;
   __shared__ WaveSmem<NW, 16, D> sm;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -117,14 +117,14 @@ paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
     sm.m[wave][w.n16] = w.m_run;
     sm.l[wave][w.n16] = w.l_run;
   }
-  // Lane holds O[g = 4j + r][d = n16*CH + m].
+  // Lane holds O[g = 4j + r][d = W::col_of(n16, m)].
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float *dst = &sm.o[wave][4 * w.j + r][w.n16 * W::CH];
+    float *dst = &sm.o[wave][4 * w.j + r][0];
 #pragma unroll
     for (int m = 0; m < W::CH; m += 4) {
       f32x4 v = {w.o[m][r], w.o[m + 1][r], w.o[m + 2][r], w.o[m + 3][r]};
-      store_vec<f32x4>(dst + m, v);
+      store_vec<f32x4>(dst + W::col_of(w.n16, m), v);
     }
   }
   __syncthreads();
@@ -245,13 +245,15 @@ hipError_t launch_reduce_t(const DecodeParams &p, hipStream_t stream) {
 }  // namespace
 
 bool decode_mfma_supported(DType dt, int head_dim, int block_size) {
-  return (dt == DType::F16 || dt == DType::BF16) && (head_dim == 64 || head_dim == 128) &&
-         block_size >= 4;
+  // fp32 runs on the fp32 MFMA wave (DecodeWaveF32).
+  return (dt == DType::F16 || dt == DType::BF16 || dt == DType::F32) &&
+         (head_dim == 64 || head_dim == 128) && block_size >= 4;
 }
 
 hipError_t launch_decode_mfma(const DecodeParams &p, DType dt, hipStream_t stream) {
   if (dt == DType::BF16) return launch_mfma_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_mfma_t<_Float16>(p, stream);
+  if (dt == DType::F32) return launch_mfma_t<float>(p, stream);
   return hipErrorInvalidValue;
 }
 

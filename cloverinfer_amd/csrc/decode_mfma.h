@@ -170,6 +170,11 @@ struct DecodeWave {
     reset();
   }
 
+  // Output column of accumulator element m in lane group n16 (o[m] holds
+  // O[g = 4j + r][col_of(n16, m)]; four consecutive m from a multiple of 4
+  // are four consecutive columns).
+  __device__ __forceinline__ static int col_of(int n16, int m) { return n16 * CH + m; }
+
   // KV8: the scales of the kv head a run reads (the key scale times the
   // softmax scale in the log2 domain, and the value scale).
   __device__ __forceinline__ void set_kv_scales(float scale_log2_k, float vs) {
@@ -444,6 +449,11 @@ struct DecodeWaveF32 {
 
   __device__ __forceinline__ void set_k_lds(char *) {}
 
+  // As DecodeWave::col_of, for this wave's column placement.
+  __device__ __forceinline__ static int col_of(int n16, int m) {
+    return 64 * (m >> 2) + 4 * n16 + (m & 3);
+  }
+
   __device__ __forceinline__ void reset() {
 #pragma unroll
     for (int m = 0; m < CH; ++m) o[m] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -465,6 +475,12 @@ struct DecodeWaveF32 {
   __device__ __forceinline__ void mask_q(const u32x4 (&raw)[NQK], int ng, qk_t (&q)[NQK]) const {
 #pragma unroll
     for (int i = 0; i < NQK; ++i) q[i] = n16 < ng ? raw[i] : (u32x4){0u, 0u, 0u, 0u};
+  }
+  __device__ __forceinline__ void load_q(const DecodeParams &p, int s, int h0, int ng,
+                                         qk_t (&q)[NQK]) const {
+    u32x4 raw[NQK];
+    load_q_raw(p, s, h0, ng, raw);
+    mask_q(raw, ng, q);
   }
 
   // UNI: the loads of the 16-token step at token `tok` of block `blk` (an
@@ -596,6 +612,16 @@ struct DecodeWaveF32 {
       }
     }
   }
+};
+
+// The per-wave decode type of the grid kernel (paged_decode_mfma).
+template <typename T, int D, bool UNI>
+struct GridWave {
+  typedef DecodeWave<T, D, UNI> type;
+};
+template <int D, bool UNI>
+struct GridWave<float, D, UNI> {
+  typedef DecodeWaveF32<D, UNI> type;
 };
 
 // The per-wave decode type of the balanced stream kernel.

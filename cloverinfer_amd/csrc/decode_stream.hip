@@ -318,10 +318,7 @@ hipError_t launch_sreduce_t(const DecodeParams &p, hipStream_t stream) {
 }  // namespace
 
 bool decode_stream_supported(DType dt, int head_dim, int block_size, int64_t num_segments) {
-  // fp32 pools run on the fp32 MFMA wave (DecodeWaveF32).
-  const bool f32 = dt == DType::F32 && (head_dim == 64 || head_dim == 128) && block_size >= 4;
-  return (f32 || decode_mfma_supported(dt, head_dim, block_size)) &&
-         num_segments <= kStreamMaxSegments;
+  return decode_mfma_supported(dt, head_dim, block_size) && num_segments <= kStreamMaxSegments;
 }
 
 bool stream_appends_in_kernel(DType dt, int head_dim, int block_size, int group) {

@@ -317,7 +317,7 @@ def bench_decode(args, cfg):
         "roofline": {
             "bound": "hbm",
             "kernel": {"balanced": "paged_decode_stream", "split": "paged_decode_mfma",
-                       "single": "paged_decode_mfma"}[mode] if cfg["dtype"] != "float32"
+                       "single": "paged_decode_mfma"}[mode] if cfg["d"] in (64, 128)
                       else "paged_decode_valu",
             "achieved": achieved,
             "peak": PEAK_HBM_GBS,

@@ -126,7 +126,7 @@ struct DecodeWave {
   // LDS row stride of the K transpose buffer: 32 mod 64 bytes keeps both the
   // row writes and the A-layout reads (lane row = lane % 16) conflict-free.
   static constexpr int KT_ROW = D * EB + 32;
-  static constexpr int KT_BYTES = 16 * KT_ROW;
+  static constexpr int KT_BYTES = KT ? 16 * KT_ROW : 16;  // 16: no transpose buffer
   static_assert(!KT || (UNI && D == 128), "K transpose needs block_size >= 16 and head_dim 128");
   static_assert(!KV8 || KT, "fp8 pools are read on the K-transpose path");
   static constexpr int EBC = KV8 ? 1 : EB;  // bytes per cache element
@@ -614,7 +614,10 @@ struct DecodeWaveF32 {
   }
 };
 
-// The per-wave decode type of the grid kernel (paged_decode_mfma).
+// The per-wave decode type of the grid kernel (paged_decode_mfma). K stays
+// in the A layout here: the K transpose of the stream kernel measured 6 %
+// slower in this kernel (16 x 32K-token split-K decode: 364 -> 387 us, also
+// at three waves per SIMD).
 template <typename T, int D, bool UNI>
 struct GridWave {
   typedef DecodeWave<T, D, UNI> type;

@@ -80,6 +80,12 @@ __device__ __forceinline__ void kt_store_row(const char *kbase, const char *vbas
   }
 }
 
+// Two e4m3 values (bytes 0, 1, or 2, 3 with hi) of w as two fp16, exact.
+__device__ __forceinline__ uint32_t cvt_fp8x2_f16(uint32_t w, bool hi) {
+  return __builtin_bit_cast(uint32_t, hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, true)
+                                         : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.f, false));
+}
+
 // Eight fp8 (OCP e4m3) values, bytes of w in order, as eight T values (exact
 // for both 16-bit types: e4m3 has 3 mantissa bits and an exponent range
 // inside theirs).
@@ -271,13 +277,10 @@ struct DecodeWave {
   __device__ __forceinline__ void compute(int base, int t_end, Regs &R, const qk_t (&q)[NQK]) {
     if constexpr (KV8) {
       // fp8 -> 16 bits, exact, eight values per row chunk (the layout of the
-      // 16-bit loads): K to T for the score MFMAs, V to fp16, which holds
-      // every e4m3 value, for the fp16 P.V below.
+      // 16-bit loads): K to T for the score MFMAs. V is converted to fp16,
+      // which holds every e4m3 value, while its B operands are built below.
 #pragma unroll
       for (int i = 0; i < NQK; ++i) R.k[i] = fp8x8_to<T>(R.k8[i]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        R.v[r] = __builtin_bit_cast(vchunk_t, fp8x8_to<_Float16>(R.v8[r]));
     }
     if constexpr (KT) {
       // R.k[i] holds row 4j + i, bytes 16 n16 .. +16 (the V pattern). Through
@@ -303,8 +306,12 @@ struct DecodeWave {
     if (!full) {
       const vchunk_t z = {};
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (x[r] == kNegInf) R.v[r] = z;  // keep NaN/Inf of unused slots out of P.V
+      for (int r = 0; r < 4; ++r) {
+        if (x[r] == kNegInf) {  // keep NaN/Inf of unused slots out of P.V
+          if constexpr (KV8) R.v8[r] = (u32x2){0u, 0u};
+          else R.v[r] = z;
+        }
+      }
     }
     float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
     mx = fmaxf(mx, shfl_xor(mx, 16));
@@ -340,11 +347,25 @@ struct DecodeWave {
       // fp8 pools: P.V in fp16, one MFMA per block. P lies in [0, 1], where
       // fp16 keeps 11 significant bits (relative rounding <= 2^-12, below
       // the rounding of a 16-bit output).
+      // B operands straight from the fp8 bytes: element m of row r is byte
+      // m & 3 of word m >> 2 of R.v8[r]; one byte permute gathers elements
+      // m, m + 1 of two rows, and each fp8 pair converts into one B word
+      // (8 permutes and 16 conversions per step instead of 16 + 16).
       typedef Mfma16x16x16<_Float16> MfH;
       const typename MfH::op_t ph = pack4<_Float16>(pf);
 #pragma unroll
-      for (int m = 0; m < CH; ++m)
-        o[m] = MfH::run(ph, __builtin_bit_cast(typename MfH::op_t, vcol(m)), o[m]);
+      for (int m = 0; m < CH; m += 2) {
+        const int w = m >> 2, a = m & 3;
+        const uint32_t sel = (uint32_t)a | (uint32_t)(a + 4) << 8 | (uint32_t)(a + 1) << 16 |
+                             (uint32_t)(a + 5) << 24;
+        // bytes (row 2c, m), (row 2c + 1, m), (row 2c, m + 1), (row 2c + 1, m + 1)
+        const uint32_t x01 = __builtin_amdgcn_perm(R.v8[1][w], R.v8[0][w], sel);
+        const uint32_t x23 = __builtin_amdgcn_perm(R.v8[3][w], R.v8[2][w], sel);
+        const u32x2 b0 = {cvt_fp8x2_f16(x01, false), cvt_fp8x2_f16(x23, false)};
+        const u32x2 b1 = {cvt_fp8x2_f16(x01, true), cvt_fp8x2_f16(x23, true)};
+        o[m] = MfH::run(ph, __builtin_bit_cast(typename MfH::op_t, b0), o[m]);
+        o[m + 1] = MfH::run(ph, __builtin_bit_cast(typename MfH::op_t, b1), o[m + 1]);
+      }
     } else {
       const pv_t pa = pack4<T>(pf);
 #pragma unroll

@@ -432,8 +432,10 @@ int clv_paged_decode_fp8(const clv_decode_args *a, const float *k_scales, const 
   if ((a->kv_stride_block & 15) || (a->kv_stride_token & 15) || (a->kv_stride_head & 15))
     return CLV_EINVAL;
   // Half the bytes per step make the per-step compute the longer part: two
-  // waves per SIMD (clv_default_num_waves_fp8) with four steps in flight.
-  p.stream_depth = stream_depth_setting(4);
+  // waves per SIMD (clv_default_num_waves_fp8) with three steps in flight
+  // (GQA-7B batch: step 0.0979 ms at depth 3, 0.0991 at depth 4; 2560 or
+  // 3072 waves at depth 3, 3072 or 4096 at depth 2: slower).
+  p.stream_depth = stream_depth_setting(3);
   p.kv_fp8 = 1;
   p.k_scales = k_scales;
   p.v_scales = v_scales;

@@ -508,13 +508,14 @@ def bench_copy(args):
                        "bytes_read_per_step": n, "bytes_written_per_step": n}}
 
 
-def bench_node(args, dtype_name="bfloat16"):
+def bench_node(args, dtype_name="bfloat16", packed=False):
     """The "gpu" AttentionNode backend end to end: one decode_layer_batch of
     the GQA Qwen2.5-7B shape batch (128 requests, 28 q / 4 kv heads, head_dim
     128, contexts U[256, 8192]) with the query/key/value rows on the host, as
     the node receives them; wall time per call, host work included. bf16, or
     fp32 (what the reference's CPU dense nodes send, src/core/nodes.py:21-24;
-    the pools then default to fp32)."""
+    the pools then default to fp32). packed: the same batch through
+    decode_layer_packed, the payloads stacked as [128, heads, 128] host tensors."""
     import torch
     from cloverinfer_amd.attention_backend import GpuAttentionBackend
 
@@ -537,20 +538,30 @@ def bench_node(args, dtype_name="bfloat16"):
               "key": torch.randn((1, hkv, d), generator=gh).to(dt),
               "value": torch.randn((1, hkv, d), generator=gh).to(dt),
               "score_scale": d ** -0.5} for i in range(S)]
+    if packed:
+        rids = [it["request_id"] for it in items]
+        qkv = [torch.cat([it[n] for it in items]) for n in ("query", "key", "value")]
+
+        def call():
+            return be.decode_layer_packed(rids, 0, *qkv, d ** -0.5)
+    else:
+        def call():
+            return be.decode_layer_batch(items)
     for _ in range(args.warmup):
-        be.decode_layer_batch(items)
+        call()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        be.decode_layer_batch(items)
+        call()
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) / args.steps * 1e3
-    return {"metric": "gpu AttentionNode backend: decode_layer_batch wall time per layer",
+    api = "decode_layer_packed" if packed else "decode_layer_batch"
+    return {"metric": f"gpu AttentionNode backend: {api} wall time per layer",
             "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
             "dtype": {"bfloat16": "bf16", "float32": "f32"}[dtype_name],
             "data": "synthetic N(0,1), seeded; q/k/v rows on the host",
-            "config": {"workload": "decode_layer_batch of 128 requests, GQA Qwen2.5-7B shape, "
+            "config": {"workload": f"{api} of 128 requests, GQA Qwen2.5-7B shape, "
                                    "contexts U[256,8192], one layer, host-side q/k/v"},
             "requests_per_s": S / (ms * 1e-3)}
 
@@ -564,7 +575,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="qwen7b",
                     choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node",
-                                                      "node_fp32"])
+                                                      "node_fp32", "node_packed"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass, -1 or default: automatic)")
     ap.add_argument("--waves", type=int, default=0,
@@ -593,6 +604,8 @@ def main() -> int:
         result = bench_node(args)
     elif args.config == "node_fp32":
         result = bench_node(args, "float32")
+    elif args.config == "node_packed":
+        result = bench_node(args, packed=True)
     else:
         result = bench_decode(args, DECODE_CONFIGS[args.config])
     print(json.dumps(result), flush=True)

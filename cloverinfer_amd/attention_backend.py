@@ -322,7 +322,7 @@ class GpuAttentionBackend:
             if len(layers) == 1 and len(scales) == 1:
                 reqs = [requests.get(it["request_id"]) for it in items]
                 if None not in reqs and len({r.row for r in reqs}) == len(reqs):
-                    return self._run_wave(list(items), reqs, int(layers.pop()),
+                    return self._run_wave(*self._payloads(items), reqs, int(layers.pop()),
                                           float(scales.pop()))
         out: List[torch.Tensor] = []
         wave: List[Dict[str, object]] = []
@@ -338,15 +338,47 @@ class GpuAttentionBackend:
                     raise KeyError(f"Unknown request {rid}")
             k = (int(it["layer_idx"]), float(it.get("score_scale", 1.0)))
             if wave and (k != key or req.row in in_wave):
-                out.extend(self._run_wave(wave, reqs, *key))
+                out.extend(self._run_wave(*self._payloads(wave), reqs, *key))
                 wave, reqs, in_wave = [], [], set()
             key = k
             wave.append(it)
             reqs.append(req)
             in_wave.add(req.row)
         if wave:
-            out.extend(self._run_wave(wave, reqs, *key))
+            out.extend(self._run_wave(*self._payloads(wave), reqs, *key))
         return out
+
+    @staticmethod
+    def _payloads(items: List[Dict[str, object]]):
+        return ([it["query"] for it in items], [it["key"] for it in items],
+                [it["value"] for it in items])
+
+    def decode_layer_packed(self, request_ids: List[str], layer_idx: int, query: torch.Tensor,
+                            key: torch.Tensor, value: torch.Tensor,
+                            score_scale: float = 1.0) -> torch.Tensor:
+        """decode_layer_batch for one layer of distinct requests with the
+        payloads stacked: query [B, Hq, D], key / value [B, Hkv, D] (host or
+        device) -> contexts [B, 1, Hq, D] in the query's dtype and on its
+        device. Row i is exactly what decode_layer_batch returns for item i;
+        the stacked form spares the per-tensor cost of B separate payloads
+        and outputs."""
+        n = len(request_ids)
+        if query.dim() != 3 or query.shape[0] != n or key.shape[0] != n or value.shape[0] != n:
+            raise ValueError("query, key and value need one row per request id")
+        reqs = []
+        for rid in request_ids:
+            req = self.requests.get(rid)
+            if req is None:
+                req = self.requests.get(str(rid))
+                if req is None:
+                    raise KeyError(f"Unknown request {rid}")
+            reqs.append(req)
+        if len({r.row for r in reqs}) != n:
+            raise ValueError("decode_layer_packed takes each request at most once")
+        if n == 0:
+            return query.new_empty((0, 1) + tuple(query.shape[1:]))
+        return self._run_wave(query, key, value, reqs, int(layer_idx), float(score_scale),
+                              packed=True)
 
     def _staging(self, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
         """A pinned host buffer of at least ``shape``, reused across calls (the
@@ -369,6 +401,13 @@ class GpuAttentionBackend:
         n = len(ts)
         t0 = ts[0]
         host = raw.view(dt).view(n, heads, d)
+        if isinstance(ts, torch.Tensor):  # stacked payloads
+            if ts.numel() != n * heads * d:
+                raise ValueError(f"payload of shape {tuple(ts.shape)}, expected {n} x {heads} x {d}")
+            if ts.is_cuda:
+                return ts.reshape(n, heads, d).to(device=self.device, dtype=dt)
+            host.copy_(ts.reshape(n, heads, d))
+            return None
         if t0.device.type == "cpu" and t0.numel() == heads * d:
             # The node's case (host tensors of one shape): one stack straight
             # into the pinned buffer; torch checks shapes and devices (and
@@ -386,17 +425,16 @@ class GpuAttentionBackend:
         host.copy_(torch.stack([t.reshape(heads, d).to("cpu") for t in ts]))
         return None
 
-    def _run_wave(self, items: List[Dict[str, object]], reqs: List[_Request], layer: int,
-                  score_scale: float) -> List[torch.Tensor]:
+    def _run_wave(self, qs, ks, vs, reqs: List[_Request], layer: int, score_scale: float,
+                  packed: bool = False):
+        """One append + decode over distinct requests. qs / ks / vs: lists of
+        per-request payloads, or stacked tensors (packed; returns one tensor)."""
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"layer_idx {layer} outside [0, {self.num_layers})")
         _, _, bs, hkv, d = self.k_pools.shape
         if self._stage_done is not None:
             self._stage_done.synchronize()  # the staging buffer is free again
-        n = len(items)
-        qs = [it["query"] for it in items]
-        ks = [it["key"] for it in items]
-        vs = [it["value"] for it in items]
+        n = len(reqs)
         q0 = qs[0]
         hq = q0.numel() // d
         dt = self._compute_dtype(q0.dtype)
@@ -471,6 +509,8 @@ class GpuAttentionBackend:
         # Outputs in each query's dtype and on its device: one copy for the
         # batch when the queries agree (the node's case), per item otherwise.
         qdt, qdev = q0.dtype, q0.device
+        if packed:
+            return ctx_out.to(device=qdev, dtype=qdt).view(n, 1, hq, d)
         if all(t.dtype == qdt for t in qs) and (
                 (qdev.type == "cpu" and all(not t.is_cuda for t in qs))
                 or all(t.device == qdev for t in qs)):

@@ -236,3 +236,47 @@ def test_many_requests_long_rows_mixed_batches():
     for rid in rids:
         assert gpu.get_context_len(rid) == cpu.get_context_len(rid)
     assert gpu.tables.table.shape[0] >= 80 and gpu.tables.width >= 70
+
+
+@pytest.mark.parametrize("kv_dtype,dtype", [(None, torch.bfloat16), ("fp32", torch.float32),
+                                            ("fp8", torch.bfloat16)])
+def test_packed_batch_equals_item_batch(kv_dtype, dtype):
+    """decode_layer_packed (stacked payloads, host or device) returns exactly
+    the rows decode_layer_batch returns for the same items, and leaves the
+    pools, tables and context lengths in the same state."""
+    g = torch.Generator().manual_seed(53)
+    hq, hkv, d, layers, bs = 28, 4, 128, 2, 16
+    kw = {"num_blocks": 512, "block_size": bs}
+    if kv_dtype:
+        kw["kv_dtype"] = kv_dtype
+    a, b = GpuAttentionBackend(**kw), GpuAttentionBackend(**kw)
+    lens = [0, 1, 15, 16, 17, 200, 513, 96]
+    rids = [f"p{i}" for i in range(len(lens))]
+    for rid, T in zip(rids, lens):
+        kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(T, hkv, d, generator=g).to(dtype)} for _ in range(layers)]
+        assert a.init_request(rid, kv) == b.init_request(rid, kv) == T
+    for step in range(3):
+        dev = "cuda" if step == 1 else "cpu"
+        order = rids[step:] + rids[:step]  # a different row order per step
+        for layer in range(layers):
+            q = torch.randn(len(order), hq, d, generator=g).to(dtype).to(dev)
+            k = torch.randn(len(order), hkv, d, generator=g).to(dtype).to(dev)
+            v = torch.randn(len(order), hkv, d, generator=g).to(dtype).to(dev)
+            items = [{"request_id": r, "layer_idx": layer, "query": q[i:i + 1],
+                      "key": k[i:i + 1], "value": v[i:i + 1], "score_scale": d ** -0.5}
+                     for i, r in enumerate(order)]
+            ref = a.decode_layer_batch(items)
+            got = b.decode_layer_packed(order, layer, q, k, v, d ** -0.5)
+            assert got.shape == (len(order), 1, hq, d) and got.dtype == dtype
+            assert got.device.type == dev
+            assert torch.equal(got, torch.stack(ref)), f"step {step} layer {layer}"
+    assert torch.equal(a.k_pools, b.k_pools) and torch.equal(a.v_pools, b.v_pools)
+    assert [a.get_context_len(r) for r in rids] == [b.get_context_len(r) for r in rids]
+    assert all(a.get_context_len(r) == T + 3 for r, T in zip(rids, lens))
+    with pytest.raises(ValueError, match="at most once"):
+        b.decode_layer_packed([rids[0], rids[0]], 0, q[:2], k[:2], v[:2])
+    with pytest.raises(KeyError):
+        b.decode_layer_packed(["nope"], 0, q[:1], k[:1], v[:1])
+    with pytest.raises(ValueError, match="one row per request"):
+        b.decode_layer_packed(rids[:2], 0, q[:3], k[:2], v[:2])

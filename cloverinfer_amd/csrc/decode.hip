@@ -211,7 +211,9 @@ hipError_t launch_mfma_tdw(const DecodeParams &p, hipStream_t stream) {
 }
 
 // Waves per workgroup: a single pass splits each (possibly long) context over
-// four waves; split-K already has a workgroup per partition, and one wave
+// four waves (kernel us with 2 / 4 / 8 waves: ragged GQA-7B bf16 303 / 242 /
+// 239, MHA Llama-7B fp16 377 / 346 / 355, GQA-7B over fp32 447 / 430 / 437);
+// split-K already has a workgroup per partition, and one wave
 // each measured best there (partition 512; kernel us with 4 / 2 / 1 waves:
 // 16 x 32K-token fp16 365 / 358 / 358, the ragged GQA-7B bf16 batch
 // 286 / 274 / 270, the same over fp32 pools 574 / 511 / 484; 8 waves: 414

@@ -405,7 +405,9 @@ class GpuAttentionBackend:
             if ts.numel() != n * heads * d:
                 raise ValueError(f"payload of shape {tuple(ts.shape)}, expected {n} x {heads} x {d}")
             if ts.is_cuda:
-                return ts.reshape(n, heads, d).to(device=self.device, dtype=dt)
+                # reshape() of a strided view can keep a strided head_dim,
+                # which the kernels refuse: make it contiguous.
+                return ts.reshape(n, heads, d).to(device=self.device, dtype=dt).contiguous()
             host.copy_(ts.reshape(n, heads, d))
             return None
         if t0.device.type == "cpu" and t0.numel() == heads * d:
@@ -422,86 +424,113 @@ class GpuAttentionBackend:
                 t.shape == t0.shape and t.is_cuda and (idx is None or t.get_device() == idx)
                 for t in ts):
             return torch.stack(ts).view(n, heads, d).to(dt)
+        for t in ts:
+            if t.numel() != heads * d:
+                raise ValueError(f"payload of shape {tuple(t.shape)}, expected {heads} x {d}")
         host.copy_(torch.stack([t.reshape(heads, d).to("cpu") for t in ts]))
         return None
 
     def _run_wave(self, qs, ks, vs, reqs: List[_Request], layer: int, score_scale: float,
                   packed: bool = False):
         """One append + decode over distinct requests. qs / ks / vs: lists of
-        per-request payloads, or stacked tensors (packed; returns one tensor)."""
+        per-request payloads, or stacked tensors (packed; returns one tensor).
+
+        Payloads are validated and staged before any request state changes:
+        a malformed call raises and leaves every request as it was (the
+        reference backend raises from torch.cat before it appends anything,
+        src/core/attention_backend.py:105-110). Should a later step fail,
+        the token counts are rolled back and the block-table entries queued
+        again."""
         if not 0 <= layer < self.num_layers:
             raise IndexError(f"layer_idx {layer} outside [0, {self.num_layers})")
         _, _, bs, hkv, d = self.k_pools.shape
-        if self._stage_done is not None:
-            self._stage_done.synchronize()  # the staging buffer is free again
         n = len(reqs)
         q0 = qs[0]
         hq = q0.numel() // d
+        if hq * d != q0.numel() or hq == 0 or hq % hkv:
+            raise ValueError(f"query of shape {tuple(q0.shape)}: expected [{hkv}*G, {d}] rows "
+                             f"for {hkv} kv heads of head_dim {d}")
+        if self._stage_done is not None:
+            self._stage_done.synchronize()  # the staging buffer is free again
         dt = self._compute_dtype(q0.dtype)
         kdt = self._append_dtype(ks[0].dtype)  # fp8 pools: quantised once, from the payload
+
+        # One pinned buffer, one upload: q | k | v | int32 context lengths and
+        # rows | int64 slots and table updates (rows, columns, blocks). The
+        # table updates come last: their count is known only after the
+        # bookkeeping, and a wave takes at most one new block per request.
+        qb = n * hq * d * torch.finfo(dt).bits // 8
+        kb = n * hkv * d * torch.finfo(kdt).bits // 8
+        o_k = _align(qb)
+        o_v = o_k + _align(kb)
+        o_i = o_v + _align(kb)
+        o_w = o_i + _align(8 * n)
+        nu_max = self.tables.pending_count() + n
+        buf = self._staging("wave", (o_w + 8 * (n + 3 * nu_max),), torch.uint8)
+        q = self._fill(qs, hq, d, dt, buf[:qb])
+        k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
+        v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
 
         # Bookkeeping over the requests' rows: the new token of request i
         # goes to position pos[i] of this layer (a request whose blocks are
         # full takes one more first).
         rows = np.fromiter((r.row for r in reqs), dtype=np.int64, count=n)
         pos = self._lens[rows, layer]
-        for i in np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist():
+        full = np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist()
+        if len(full) > len(self.free_blocks):
+            raise RuntimeError("OOM during append")
+        for i in full:
             self._grow_request(reqs[i])
         slots = self._htab[rows, pos >> self._bshift] * bs + (pos & (bs - 1))
         lens = pos + 1
         self._lens[rows, layer] = lens
         upd = self.tables.take_pending()
         nu = len(upd)
-
-        # One pinned buffer, one upload: q | k | v | int64 slots and table
-        # updates (rows, columns, blocks) | int32 context lengths and rows.
-        qb = n * hq * d * torch.finfo(dt).bits // 8
-        kb = n * hkv * d * torch.finfo(kdt).bits // 8
-        o_k = _align(qb)
-        o_v = o_k + _align(kb)
-        o_w = o_v + _align(kb)
-        o_i = o_w + _align(8 * (n + 3 * nu))
-        total = o_i + 8 * n
-        buf = self._staging("wave", (total,), torch.uint8)
-        q = self._fill(qs, hq, d, dt, buf[:qb])
-        k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
-        v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
-        wide = buf[o_w:o_w + 8 * (n + 3 * nu)].numpy().view(np.int64)
-        wide[:n] = slots
-        if nu:
-            wide[n:] = np.asarray(upd, dtype=np.int64).T.reshape(-1)
-        narrow = buf[o_i:total].numpy().view(np.int32)
-        narrow[:n] = lens
-        narrow[n:] = rows
-        dev = buf.to(self.device, non_blocking=True)
-        self._stage_done = torch.cuda.Event()
-        self._stage_done.record()
-        if q is None:
-            q = dev[:qb].view(dt).view(n, hq, d)
-        if k is None:
-            k = dev[o_k:o_k + kb].view(kdt).view(n, hkv, d)
-        if v is None:
-            v = dev[o_v:o_v + kb].view(kdt).view(n, hkv, d)
-        wide_dev = dev[o_w:o_w + 8 * (n + 3 * nu)].view(torch.int64)
-        if nu:
-            self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
-        slots_dev = wide_dev[:n]
-        narrow_dev = dev[o_i:total].view(torch.int32)
-        ctx_dev = narrow_dev[:n]
-        bt = self.tables.rows(rows.tolist(), narrow_dev[n:])
-        ctx_out = torch.empty_like(q)
-        kp, vp = self.k_pools[layer], self.v_pools[layer]
-        max_len = int(lens.max())
-        if self.partition_size is None and kernels.append_fusable(q, kp, n):
-            # Append and decode in one call: the new rows land at position
-            # lens - 1, the slots computed above.
-            kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len, k, v,
-                                           scale=score_scale)
-        else:
-            self._append(k, v, layer, slots_dev)
-            kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
-                                    scale=score_scale, partition_size=self.partition_size,
-                                    k_scale=self.k_scales, v_scale=self.v_scales)
+        applied = False
+        try:
+            total = o_w + 8 * (n + 3 * nu)
+            narrow = buf[o_i:o_i + 8 * n].numpy().view(np.int32)
+            narrow[:n] = lens
+            narrow[n:] = rows
+            wide = buf[o_w:total].numpy().view(np.int64)
+            wide[:n] = slots
+            if nu:
+                wide[n:] = np.asarray(upd, dtype=np.int64).T.reshape(-1)
+            dev = buf[:total].to(self.device, non_blocking=True)
+            self._stage_done = torch.cuda.Event()
+            self._stage_done.record()
+            if q is None:
+                q = dev[:qb].view(dt).view(n, hq, d)
+            if k is None:
+                k = dev[o_k:o_k + kb].view(kdt).view(n, hkv, d)
+            if v is None:
+                v = dev[o_v:o_v + kb].view(kdt).view(n, hkv, d)
+            wide_dev = dev[o_w:total].view(torch.int64)
+            if nu:
+                self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
+            applied = True
+            slots_dev = wide_dev[:n]
+            narrow_dev = dev[o_i:o_i + 8 * n].view(torch.int32)
+            ctx_dev = narrow_dev[:n]
+            bt = self.tables.rows(rows.tolist(), narrow_dev[n:])
+            ctx_out = torch.empty_like(q)
+            kp, vp = self.k_pools[layer], self.v_pools[layer]
+            max_len = int(lens.max())
+            if self.partition_size is None and kernels.append_fusable(q, kp, n):
+                # Append and decode in one call: the new rows land at position
+                # lens - 1, the slots computed above.
+                kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len, k, v,
+                                               scale=score_scale)
+            else:
+                self._append(k, v, layer, slots_dev)
+                kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
+                                        scale=score_scale, partition_size=self.partition_size,
+                                        k_scale=self.k_scales, v_scale=self.v_scales)
+        except BaseException:
+            self._lens[rows, layer] = pos
+            if not applied:
+                self.tables.requeue(upd)
+            raise
         if layer == self.num_layers - 1:
             self._ctx[rows] += 1
         self.stats["decode_items"] += n

@@ -65,6 +65,14 @@ class DeviceBlockTable:
             self.apply(torch.tensor(upd, dtype=torch.int64).t().contiguous().to(self.device),
                        max(c for _, c, _ in upd))
 
+    def pending_count(self) -> int:
+        return len(self._pending)
+
+    def requeue(self, upd: List[Tuple[int, int, int]]) -> None:
+        """Put entries handed out by ``take_pending`` back in front of the
+        queue (their upload did not happen)."""
+        self._pending = list(upd) + self._pending
+
     def take_pending(self) -> List[Tuple[int, int, int]]:
         """Hand the queued entries to a caller that uploads them itself (with
         other data), then applies them with ``apply``."""

@@ -1,11 +1,16 @@
 // clover_attn_abi.hip - the extern "C" boundary declared in include/clover_attn.h.
 //
 // Validates every argument block, turns it into the kernels' parameter
-// structs and dispatches. Nothing here allocates device memory or keeps state
-// between calls; errors come back as status codes.
+// structs and dispatches. Nothing here allocates device memory; the only
+// state kept between calls is per-device: the compute-unit count and the
+// address of the fixed scratch array of clv_paged_decode_balanced_noalloc.
+// Errors come back as status codes.
 #include <math.h>
 #include <stddef.h>
 #include <stdlib.h>
+
+#include <atomic>
+#include <mutex>
 
 #include "clover_attn.h"
 #include "clv_internal.h"
@@ -35,6 +40,27 @@ bool stride16(int64_t stride, int eb) { return (stride * eb) % 16 == 0; }
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Compute units of the current device, queried once per device and cached
+// (the default wave counts depend on it). 0 is "not queried yet"; a failed
+// query answers 256 (MI355X) without caching.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_device_cus[kMaxDevices];
+
+int device_compute_units() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < kMaxDevices) {
+    const int c = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;
+  if (dev < kMaxDevices) g_device_cus[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 // Validates a decode argument block and fills the kernel parameters.
 int fill_decode(const clv_decode_args *a, clv::DecodeParams *p) {
@@ -278,14 +304,10 @@ int clv_paged_decode_splitk(const clv_decode_args *a, int32_t partition_size, vo
 }
 
 int32_t clv_default_num_waves(void) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 1024;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 1024;
-  // One wave per SIMD (4 per compute unit), each keeping four steps of loads
-  // in flight: on MI355X this streams the paged cache faster than more waves
-  // with shallower pipelines.
-  return cus * 4;
+  // One wave per SIMD (4 per compute unit), each keeping three steps of
+  // loads in flight: on MI355X this streams the paged cache faster than more
+  // waves with shallower pipelines.
+  return device_compute_units() * 4;
 }
 
 int32_t clv_default_num_waves_fp8(void) { return 2 * clv_default_num_waves(); }
@@ -307,28 +329,30 @@ size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads, int32_t
 namespace {
 
 // Ring depth of the balanced decode: steps of loads each wave keeps in
-// flight (2, 3, 4 or 6). CLV_STREAM_DEPTH overrides the default for tuning.
-int stream_depth_setting(int def = 3) {
-  const char *env = getenv("CLV_STREAM_DEPTH");
-  if (env) {
-    const int d = atoi(env);
-    if (d == 2 || d == 3 || d == 4 || d == 6) return d;
-  }
+// flight (2, 3, 4 or 6): three for 16-bit and fp8 pools, two for fp32 pools
+// (twice the bytes per step). Fixed at build time; a tuning build may set
+// CLV_STREAM_DEPTH (a preprocessor value) to force one depth for every dtype.
+int stream_depth_setting(int def) {
+#ifdef CLV_STREAM_DEPTH
+  (void)def;
+  static_assert(CLV_STREAM_DEPTH == 2 || CLV_STREAM_DEPTH == 3 || CLV_STREAM_DEPTH == 4 ||
+                    CLV_STREAM_DEPTH == 6,
+                "ring depth 2, 3, 4 or 6");
+  return CLV_STREAM_DEPTH;
+#else
   return def;
+#endif
 }
 
 // Phantom steps the balanced decode charges for each segment a wave starts
 // (a run start costs one memory latency, about two 16-token steps on MI355X:
-// measured per-wave durations grow by ~2.5 us per extra run).
-// CLV_STREAM_RUN_COST overrides the default for tuning.
-int stream_run_cost_setting() {
-  const char *env = getenv("CLV_STREAM_RUN_COST");
-  if (env) {
-    const int c = atoi(env);
-    if (c >= 0 && c <= 64) return c;
-  }
-  return 2;
-}
+// measured per-wave durations grow by ~2.5 us per extra run). Fixed at build
+// time (preprocessor value CLV_STREAM_RUN_COST, default 2).
+#ifndef CLV_STREAM_RUN_COST
+#define CLV_STREAM_RUN_COST 2
+#endif
+static_assert(CLV_STREAM_RUN_COST >= 0 && CLV_STREAM_RUN_COST <= 64, "run cost 0..64 steps");
+constexpr int kStreamRunCost = CLV_STREAM_RUN_COST;
 
 // Validates a balanced-decode call and lays the workspace out in p.
 int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
@@ -350,7 +374,7 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   p->num_waves = num_waves;
   // fp32 steps are twice the bytes: two steps in flight (a sweep over 2-4).
   p->stream_depth = stream_depth_setting(a->dtype == CLV_F32 ? 2 : 3);
-  p->stream_run_cost = stream_run_cost_setting();
+  p->stream_run_cost = kStreamRunCost;
   p->num_segments = (int32_t)nseg;
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);

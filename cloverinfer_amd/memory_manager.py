@@ -164,27 +164,74 @@ class KVCacheManager:
     def write_new_kv_batch(self, request_ids: Sequence[str], k: torch.Tensor,
                            v: torch.Tensor) -> None:
         """Append one token per request (``k``/``v`` ``[B, num_kv_heads, head_dim]``)
-        with one launch; equal to ``write_new_kv`` per request in order."""
+        with one launch; equal to ``write_new_kv`` per request in order.
+        All or nothing: a batch that would run out of blocks raises the
+        reference's OOM error before any request advances."""
         self._require_gpu("write_new_kv_batch")
+        if k.shape[0] != len(request_ids) or v.shape[0] != len(request_ids):
+            raise ValueError("k and v need one row per request id")
+        if self._blocks_needed(request_ids) > len(self.free_blocks):
+            raise RuntimeError("OOM during append")
         slots = []
         for rid in request_ids:
             blk, off = self.append_slot(rid)
             slots.append(blk * self.block_size + off)
         self._write(slots, k, v)
 
-    def attention(self, q: torch.Tensor, request_ids: List[str],
-                  partition_size: Optional[int] = None) -> torch.Tensor:
-        """Paged decode for ``q [num_seqs, num_heads, head_dim]`` (memory_manager.py:175-190)."""
+    def _blocks_needed(self, request_ids: Sequence[str]) -> int:
+        """New blocks that appending one token per listed request (in order)
+        takes from the free list; a request listed twice may need a block for
+        its second token only. KeyError for an unknown request, as
+        append_slot."""
+        lens: Dict[str, int] = {}
+        held: Dict[str, int] = {}
+        need = 0
+        for rid in request_ids:
+            if rid not in lens:
+                lens[rid] = self.context_lens[rid]
+                held[rid] = len(self.block_tables[rid])
+            if lens[rid] >= held[rid] * self.block_size:
+                held[rid] += 1
+                need += 1
+            lens[rid] += 1
+        return need
+
+    def _decode(self, q: torch.Tensor, request_ids: List[str],
+                partition_size: Optional[int]) -> torch.Tensor:
+        """Paged decode of ``q`` over the requests' contexts; the result has
+        q's dtype and device (the kernels compute in the pool dtype)."""
         self._require_gpu("attention")
         lens = [self.context_lens[r] for r in request_ids]
         block_tables = self._dev_tables.rows([self._dev_rows[r] for r in request_ids])
         ctx_lens = torch.tensor(lens, dtype=torch.int32).to(self.device)
         max_len = max(lens, default=0)
-        q = q.to(device=self.device, dtype=self.dtype)
-        if not q.is_contiguous():
-            q = q.contiguous()
-        out = torch.empty_like(q)
-        kernels.paged_attention(out, q, self.k_cache, self.v_cache, block_tables, ctx_lens,
+        qk = q.to(device=self.device, dtype=self.dtype)
+        if not qk.is_contiguous():
+            qk = qk.contiguous()
+        out = torch.empty_like(qk)
+        kernels.paged_attention(out, qk, self.k_cache, self.v_cache, block_tables, ctx_lens,
                                 self.block_size, max_len, scale=self.scale,
                                 partition_size=partition_size)
+        if out.dtype != q.dtype or out.device != q.device:
+            out = out.to(device=q.device, dtype=q.dtype)
         return out
+
+    def attention(self, q: torch.Tensor, request_ids: List[str],
+                  partition_size: Optional[int] = None) -> torch.Tensor:
+        """Paged decode for ``q [num_seqs, num_heads, head_dim]`` (memory_manager.py:175-190).
+
+        Returns a tensor like ``q`` (its dtype and device), as the reference's
+        ``out = torch.empty_like(q)``. A query whose dtype differs from the
+        pool dtype is converted to it first, and the result back to q's dtype.
+        ``partition_size``: None picks the schedule (see
+        ``kernels.paged_attention``)."""
+        return self._decode(q, request_ids, partition_size)
+
+    def _paged_attention_ref(self, q: torch.Tensor, request_ids: List[str]) -> torch.Tensor:
+        """The reference's second path for the same attention
+        (memory_manager.py:192-239, called by tests/verify_attention.py:124 to
+        check the kernel): here the single-pass HIP kernel, one workgroup per
+        (sequence, kv head) over the whole context, against which the default
+        schedule of ``attention`` can be compared. Same result contract as
+        ``attention``."""
+        return self._decode(q, request_ids, 0)

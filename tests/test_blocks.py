@@ -120,3 +120,29 @@ def test_data_path_refuses_cpu():
         m.write_new_kv("a", torch.randn(2, 8), torch.randn(2, 8))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         m.load_initial_kv("b", torch.randn(3, 2, 8), torch.randn(3, 2, 8))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        m._paged_attention_ref(torch.randn(1, 2, 8), ["a"])
+
+
+def test_batch_append_block_count():
+    """write_new_kv_batch counts the blocks a batch takes before appending
+    anything (all or nothing): a request listed twice takes a block for the
+    token that crosses its border only, and the count equals what the same
+    appends one by one take from the free list."""
+    for lens, order in (([3, 4, 0], ["a", "b", "c"]), ([3, 3], ["a", "a", "b", "a"]),
+                        ([7, 8], ["b", "b", "b", "b", "b"])):
+        m = _mgr(64, 4)
+        for rid, T in zip("abc", lens):
+            m.allocate(rid, T)
+        need = m._blocks_needed(order)
+        free0 = len(m.free_blocks)
+        for rid in order:
+            m.append_slot(rid)
+        assert free0 - len(m.free_blocks) == need
+    m = _mgr(3, 4)
+    for rid in "ab":
+        m.allocate(rid, 3)  # one block each
+        m.append_slot(rid)  # now full
+    assert m._blocks_needed(["a", "b"]) == 2 > len(m.free_blocks) == 1
+    with pytest.raises(KeyError):
+        m._blocks_needed(["zz"])

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from cloverinfer_amd.attention_backend import GpuAttentionBackend, create_attention_backend
+from oracle import attention as oa
 from oracle.attention import CpuAttentionOracle
 from tests.helpers import assert_attention_close
 
@@ -280,3 +281,107 @@ def test_packed_batch_equals_item_batch(kv_dtype, dtype):
         b.decode_layer_packed(["nope"], 0, q[:1], k[:1], v[:1])
     with pytest.raises(ValueError, match="one row per request"):
         b.decode_layer_packed(rids[:2], 0, q[:3], k[:2], v[:2])
+
+
+def test_malformed_payload_leaves_state_unchanged():
+    """A decode call with a malformed payload (wrong kv-head count, a query
+    whose heads are no multiple of the kv heads, a short key) raises and
+    changes nothing: later valid steps, including ones that cross a block
+    border and take a new block, still match the restated
+    CpuAttentionBackend, and the context lengths agree."""
+    g = torch.Generator().manual_seed(61)
+    hq, hkv, d, dtype, bs = 8, 2, 64, torch.bfloat16, 16
+    gpu = GpuAttentionBackend(num_blocks=64, block_size=bs)
+    cpu = CpuAttentionOracle()
+    lens = [15, 16, 31]  # each request's next token opens a new block within two steps
+    rids = [f"x{i}" for i in range(len(lens))]
+    for rid, T in zip(rids, lens):
+        kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),
+               "value": torch.randn(T, hkv, d, generator=g).to(dtype)}]
+        assert gpu.init_request(rid, kv) == cpu.init_request(rid, kv) == T
+
+    def items(bad=None):
+        out = []
+        for i, rid in enumerate(rids):
+            it = {"request_id": rid, "layer_idx": 0,
+                  "query": torch.randn(1, hq, d, generator=g).to(dtype),
+                  "key": torch.randn(1, hkv, d, generator=g).to(dtype),
+                  "value": torch.randn(1, hkv, d, generator=g).to(dtype), "score_scale": 0.125}
+            if bad is not None and i == len(rids) - 1:
+                it[bad[0]] = bad[1]
+            out.append(it)
+        return out
+
+    free0 = len(gpu.free_blocks)
+    for bad in (("key", torch.randn(1, hkv + 1, d).to(dtype)),
+                ("value", torch.randn(hkv, d - 8).to(dtype)),
+                ("query", torch.randn(1, hq + 1, d).to(dtype))):
+        with pytest.raises((ValueError, RuntimeError)):
+            gpu.decode_layer_batch(items(bad))
+        with pytest.raises((ValueError, RuntimeError)):
+            q = torch.randn(len(rids), hq, d).to(dtype)
+            k = torch.randn(len(rids), hkv, d).to(dtype)
+            gpu.decode_layer_packed(rids, 0, q, k[:, :1] if bad[0] != "query" else k,
+                                    k if bad[0] != "query" else k, 0.125)
+    assert len(gpu.free_blocks) == free0
+    assert [gpu.get_context_len(r) for r in rids] == lens
+    for step in range(3):
+        it = items()
+        for a, b in zip(gpu.decode_layer_batch(it), cpu.decode_layer_batch(it)):
+            assert_attention_close(a, b, what=f"step {step} after the refused calls")
+    assert [gpu.get_context_len(r) for r in rids] == [cpu.get_context_len(r) for r in rids]
+
+
+def test_packed_strided_device_payloads():
+    """Stacked device payloads that are strided views (a transposed buffer,
+    head_dim not contiguous until copied) give the same rows as the
+    contiguous ones."""
+    g = torch.Generator().manual_seed(62)
+    hq, hkv, d, dtype = 8, 2, 128, torch.float16
+    a = GpuAttentionBackend(num_blocks=64, block_size=16)
+    b = GpuAttentionBackend(num_blocks=64, block_size=16)
+    for be in (a, b):
+        g2 = torch.Generator().manual_seed(63)
+        for i, T in enumerate((5, 40)):
+            be.init_request(f"s{i}", [{"key": torch.randn(T, hkv, d, generator=g2).to(dtype),
+                                       "value": torch.randn(T, hkv, d, generator=g2).to(dtype)}])
+    rids = ["s0", "s1"]
+    q = torch.randn(2, hq, d, generator=g).to(dtype).cuda()
+    k = torch.randn(2, hkv, d, generator=g).to(dtype).cuda()
+    v = torch.randn(2, hkv, d, generator=g).to(dtype).cuda()
+    qt = q.permute(2, 0, 1).contiguous().permute(1, 2, 0)  # same values, stride(2) != 1
+    kt = k.permute(2, 0, 1).contiguous().permute(1, 2, 0)
+    vt = v.permute(2, 0, 1).contiguous().permute(1, 2, 0)
+    assert qt.stride(2) != 1 and torch.equal(qt, q)
+    ref = a.decode_layer_packed(rids, 0, q, k, v, 0.1)
+    got = b.decode_layer_packed(rids, 0, qt, kt, vt, 0.1)
+    assert torch.equal(got, ref)
+    assert torch.equal(a.k_pools, b.k_pools) and torch.equal(a.v_pools, b.v_pools)
+
+
+@pytest.mark.parametrize("pool", ["bf16", "fp16"])
+def test_fp32_queries_over_16bit_pools_unrounded_oracle(pool):
+    """fp32 payloads over 16-bit pools: the backend computes with q rounded to
+    the pool dtype and rounds the output to it before returning fp32. Checked
+    against the oracle fed the fp32 query unrounded and the K/V values the
+    pool holds (rounded, as any 16-bit resident KV is), output unrounded: the
+    deviation stays inside the parity bar."""
+    g = torch.Generator().manual_seed(64)
+    pool_dt = {"bf16": torch.bfloat16, "fp16": torch.float16}[pool]
+    rnd = lambda t: t.to(pool_dt).float()
+    hq, hkv, d, T = 28, 4, 128, 300
+    gpu = GpuAttentionBackend(num_blocks=64, block_size=16, kv_dtype=pool)
+    kv = [{"key": torch.randn(T, hkv, d, generator=g), "value": torch.randn(T, hkv, d, generator=g)}]
+    gpu.init_request("r", kv)
+    keys, vals = rnd(kv[0]["key"]), rnd(kv[0]["value"])
+    worst = 0.0
+    for step in range(4):
+        q = torch.randn(1, hq, d, generator=g)
+        kn, vn = torch.randn(1, hkv, d, generator=g), torch.randn(1, hkv, d, generator=g)
+        got = gpu.decode_layer("r", 0, q, kn, vn, d ** -0.5)
+        keys, vals = torch.cat([keys, rnd(kn)]), torch.cat([vals, rnd(vn)])
+        ref = oa.attend(q[0], keys, vals, d ** -0.5).unsqueeze(0)  # fp32 q, fp32 output
+        assert got.dtype == torch.float32
+        assert_attention_close(got, ref, what=f"{pool} pool step {step}")
+        worst = max(worst, (got - ref).abs().max().item())
+    print(f"fp32 queries over {pool} pools: max-abs vs the unrounded oracle {worst:.3e}")

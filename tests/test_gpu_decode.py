@@ -177,6 +177,34 @@ def test_reference_kat_identical_rows_on_gpu():
     assert torch.allclose(out[0].float().cpu(), v.float().cpu(), atol=1e-2, rtol=1e-2)
 
 
+def test_reference_check_kernel_vs_reference_flow():
+    """tests/verify_attention.py:88-136 as the reference runs it against the
+    drop-in: attention() (the default schedule) and _paged_attention_ref()
+    (the single-pass kernel) agree to allclose(atol=1e-2, rtol=1e-2), both
+    return tensors like q, and both equal the oracle. A query in another dtype
+    than the pool comes back in its own dtype."""
+    m = KVCacheManager(100, 16, 4, 32, dtype=torch.float16, device=DEV)
+    m.allocate("req_test_kernel", seq_len=0)
+    g = torch.Generator().manual_seed(10)
+    k = torch.randn(4, 32, generator=g).half().to(DEV)
+    v = torch.randn(4, 32, generator=g).half().to(DEV)
+    for _ in range(50):
+        m.write_new_kv("req_test_kernel", k, v)
+    q = torch.randn(1, 4, 32, generator=g).half().to(DEV)
+    out_kernel = m.attention(q, ["req_test_kernel"])
+    out_ref = m._paged_attention_ref(q, ["req_test_kernel"])
+    torch.cuda.synchronize()
+    for o in (out_kernel, out_ref):
+        assert o.shape == q.shape and o.dtype == q.dtype and o.device == q.device
+    assert torch.allclose(out_kernel, out_ref, atol=1e-2, rtol=1e-2)
+    ref = oa.attend(q[0].cpu(), k.cpu().expand(50, 4, 32), v.cpu().expand(50, 4, 32), 32 ** -0.5)
+    assert_attention_close(out_ref[0], ref, what="single pass")
+    q32 = q.float()
+    o32 = m.attention(q32, ["req_test_kernel"])
+    assert o32.dtype == torch.float32 and o32.device == q32.device
+    assert_attention_close(o32[0], ref, what="fp32 query over an fp16 pool")
+
+
 # ---------------------------------------------------------------- configs
 def test_config_opt125m_fp32_with_append():
     """8 seqs, 12 heads, D 64, fp32, 64-block pool in random order: 127 tokens

@@ -22,6 +22,7 @@ CLV_EINVAL = 1
 CLV_EUNSUPPORTED = 2
 CLV_ELAUNCH = 3
 CLV_EWORKSPACE = 4
+CLV_ESCRATCH = 5
 
 _c_i32 = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -146,6 +147,9 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
     ),
+    "clv_paged_decode_balanced_noalloc": (
+        ctypes.c_int, [ctypes.POINTER(DecodeArgs), _c_i32, _c_ptr],
+    ),
     "clv_paged_decode_append": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, ctypes.c_int64, ctypes.c_int64, _c_i32,
@@ -210,7 +214,7 @@ def check(code: int, what: str) -> None:
     if code == CLV_OK:
         return
     msg = f"{what}: {status_string(code)} (status {code})"
-    if code == CLV_EINVAL or code == CLV_EWORKSPACE:
+    if code in (CLV_EINVAL, CLV_EWORKSPACE, CLV_ESCRATCH):
         raise ValueError(msg)
     if code == CLV_EUNSUPPORTED:
         raise NotImplementedError(msg)

@@ -62,6 +62,37 @@ int device_compute_units() {
   return cus;
 }
 
+// Fixed scratch of clv_paged_decode_balanced_noalloc: the balanced decode's
+// workspace (segment prefix sums and per-wave partials) for callers that
+// cannot allocate. Every GPU the library runs on holds one copy for the life
+// of the process. In host code `scratch` names a host-side stand-in, never
+// the device array: only the address hipGetSymbolAddress returns for the
+// current device (scratch_address) may reach a kernel.
+static __device__ __align__(256) unsigned char scratch[CLV_NOALLOC_SCRATCH_BYTES];
+
+std::atomic<void *> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array, looked up once per
+// device (with that device current) and kept; CLV_ELAUNCH if the runtime
+// cannot resolve it.
+int scratch_address(void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CLV_ELAUNCH;
+  void *ptr = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_dev[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr)
+        return CLV_ELAUNCH;
+      g_scratch_dev[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return CLV_OK;
+}
+
 // Validates a decode argument block and fills the kernel parameters.
 int fill_decode(const clv_decode_args *a, clv::DecodeParams *p) {
   if (a == nullptr) return CLV_EINVAL;
@@ -137,6 +168,9 @@ const char *clv_status_string(int status) {
     case CLV_EUNSUPPORTED: return "unsupported configuration (head_dim, block_size or size limit)";
     case CLV_ELAUNCH: return "kernel launch failed";
     case CLV_EWORKSPACE: return "split-K workspace missing, misaligned or too small";
+    case CLV_ESCRATCH:
+      return "problem needs more than the fixed scratch of the no-allocation entry point "
+             "(CLV_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
@@ -415,6 +449,24 @@ int clv_paged_decode_balanced(const clv_decode_args *a, int32_t num_waves, void 
   const int rc = clv_balanced_partials(a, num_waves, workspace, workspace_bytes, stream);
   if (rc != CLV_OK) return rc;
   return clv_balanced_reduce(a, num_waves, workspace, workspace_bytes, stream);
+}
+
+int clv_paged_decode_balanced_noalloc(const clv_decode_args *a, int32_t num_waves,
+                                      clv_stream_t stream) {
+  if (a == nullptr) return CLV_EINVAL;
+  if (num_waves <= 0) num_waves = clv_default_num_waves();
+  // 0 for arguments the balanced decode refuses anyway (it reports them).
+  const size_t need = clv_balanced_workspace_bytes(a->num_seqs, a->num_heads, a->num_kv_heads,
+                                                   a->head_dim, num_waves);
+  if (need > (size_t)CLV_NOALLOC_SCRATCH_BYTES) return CLV_ESCRATCH;
+  void *ws = nullptr;
+  if (need > 0 && a->num_seqs > 0) {
+    const int st = scratch_address(&ws);
+    if (st != CLV_OK) return st;
+  }
+  // The stream kernel writes the prefix sums and every partial the merge
+  // reads before it reads them: nothing in the scratch has to start at zero.
+  return clv_paged_decode_balanced(a, num_waves, ws, (size_t)CLV_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const void *value_new,

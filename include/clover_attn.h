@@ -41,7 +41,8 @@ enum clv_status {
   CLV_EINVAL = 1,       /* bad shape, stride, pointer or dtype */
   CLV_EUNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim) */
   CLV_ELAUNCH = 3,      /* the HIP runtime rejected a launch */
-  CLV_EWORKSPACE = 4    /* split-K workspace missing or too small */
+  CLV_EWORKSPACE = 4,   /* split-K workspace missing or too small */
+  CLV_ESCRATCH = 5      /* too large for the no-allocation entry point's scratch */
 };
 
 /*
@@ -202,6 +203,25 @@ int clv_balanced_partials(const clv_decode_args *args, int32_t num_waves,
 int clv_balanced_reduce(const clv_decode_args *args, int32_t num_waves,
                         const void *workspace, size_t workspace_bytes,
                         clv_stream_t stream);
+
+/*
+ * clv_paged_decode_balanced without a workspace argument and without any
+ * allocation: the workspace is a fixed device array of
+ * CLV_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held for the
+ * life of the process), for callers that cannot call hipMalloc (code under
+ * HIP graph capture, tight serving loops). No counterpart in the reference.
+ * Same arguments, kernels and result as clv_paged_decode_balanced with
+ * num_waves waves (<= 0: clv_default_num_waves()). Returns CLV_ESCRATCH,
+ * launching nothing, when clv_balanced_workspace_bytes() of the call exceeds
+ * the scratch (at head_dim 128 and 1024 waves: up to 3007 (sequence, kv head,
+ * 16-query-head chunk) segments). Uses the scratch of the current device;
+ * `stream` must belong to it. Every call on a GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (on different streams, or from different
+ * threads without ordering) race and must be serialised by the caller.
+ */
+#define CLV_NOALLOC_SCRATCH_BYTES (32u << 20)
+int clv_paged_decode_balanced_noalloc(const clv_decode_args *args, int32_t num_waves,
+                                      clv_stream_t stream);
 
 /*
  * One decode step of the reference's append-then-attend protocol

@@ -33,7 +33,7 @@ def test_header_functions_exported(native_lib):
 
 def test_abi_version_and_status_strings(native_lib):
     assert native_lib.clv_abi_version() == _native.ABI_VERSION
-    for code in range(5):
+    for code in range(6):
         assert native_lib.clv_status_string(code)
     assert b"unknown" in native_lib.clv_status_string(99)
 

@@ -1,25 +1,34 @@
 #!/usr/bin/env python3
 """Benchmark of the paged-attention hot path on one MI355X.
 
-Default workload (the headline metric): paged decode at the GQA
-Qwen2.5-7B shape - 128 sequences, 28 query / 4 kv heads, head_dim 128,
-block 16, bf16, context lengths uniform in [256, 8192] (seeded per
-sequence), pool sized to the tokens + 10 %, blocks scattered at random.
-A step is one decode pass over the batch (balanced stream decode + LSE merge).
-Inputs are resident in HBM before the timed region.
+The default run measures all five workloads of the hot path, each on the
+GPU and, for comparison, on the host cores:
 
-Prints one JSON line (stdout) with the whole-job throughput in GB/s of
-algorithmic bytes (K/V read once per kv head + q + out + block tables),
-tokens/s, a roofline entry for the dominant kernel timed with HIP events on
-its own stream, and the CPU baseline: this repository's restatement of the
-reference CpuAttentionBackend (the oracle) timed on the host cores over the
-same sequences.
+  opt125m   paged decode, 8 seqs, 12 heads, head_dim 64, fp32, context 128,
+            a step = 1-token append (reshape_and_cache) + decode
+  llama7b   paged decode, 64 seqs, 32 heads, head_dim 128, fp16, context 2048
+  long32k   split-K paged decode, 16 seqs, 32 q / 8 kv heads, fp16, context
+            32768, partition 512 + the log-sum-exp reduce
+  prefill   chunked prefill, 8 seqs x (4096 cached + 512 new), 32 q / 8 kv
+            heads, bf16, a step = append of the 4096 new rows + causal prefill
+  qwen7b    (headline) paged decode, 128 seqs, 28 q / 4 kv heads, head_dim
+            128, bf16, context U[256, 8192] seeded per sequence
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen7b]
+The JSON line's top-level fields are the headline (qwen7b): whole-job GB/s of
+algorithmic bytes (K/V read once per kv head + q + out + block tables) per
+step, tokens/s, a roofline entry for the decode kernel timed with HIP events
+on the stream it runs on, and the CPU baseline (this repository's
+restatement of the reference CpuAttentionBackend, timed on the host cores
+over a bounded sample of the same batch). "configs" holds the same fields
+for every workload. Inputs are resident in HBM before any timed region.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all|NAME]
 """
 from __future__ import annotations
 
 import argparse
+import glob
+import hashlib
 import json
 import math
 import os
@@ -27,16 +36,18 @@ import platform
 import sys
 import time
 
+ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "decode-attn HBM GB/s (% of ~8 TB/s peak) + tokens/sec at GQA-7B shape, 1 GPU"
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16/fp16 MFMA
 
 DECODE_CONFIGS = {
-    # name: (num_seqs, hq, hkv, head_dim, dtype, context spec, value scale, seed, partition)
+    # name: shape, dtype, context spec, value scale, seed, schedule
     "opt125m": dict(num_seqs=8, hq=12, hkv=12, d=64, dtype="float32", ctx=("fixed", 128),
-                    vscale=1.0, seed=1001, partition=None,
+                    vscale=1.0, seed=1001, partition=None, append=True,
                     workload="paged decode, OPT-125m shape: 8 seqs, 12 heads, head_dim 64, "
-                             "block 16, fp32, context 128"),
+                             "block 16, fp32, context 128; a step appends 1 token per sequence "
+                             "(reshape_and_cache) and decodes"),
     "llama7b": dict(num_seqs=64, hq=32, hkv=32, d=128, dtype="float16", ctx=("fixed", 2048),
                     vscale=0.5, seed=1002, partition=None,
                     workload="paged decode, MHA Llama-7B shape: 64 seqs, 32 heads, head_dim 128, "
@@ -55,12 +66,44 @@ DECODE_CONFIGS = {
     "long32k": dict(num_seqs=16, hq=32, hkv=8, d=128, dtype="float16", ctx=("fixed", 32768),
                     vscale=1.0, seed=1004, partition=512,
                     workload="split-K paged decode: 16 seqs, 32 q / 8 kv heads, head_dim 128, "
-                             "block 16, fp16, context 32768, partition 512"),
+                             "block 16, fp16, context 32768, partition 512 + LSE reduce"),
 }
+
+# The default run: every workload, the headline last (earlier ones bring the
+# GPU clock up); CPU baselines after all GPU measurements.
+ALL = ["opt125m", "llama7b", "long32k", "prefill", "qwen7b"]
+CPU_BUDGET_S = {"opt125m": 5.0, "llama7b": 8.0, "long32k": 8.0, "prefill": 10.0, "qwen7b": 10.0}
+
+DTYPE_TAG = {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def sources_sha256() -> str:
+    """Hash of the kernel sources and the C ABI: a traffic figure measured
+    on other sources is stale."""
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(ROOT, "cloverinfer_amd", "csrc", "*")) +
+                   glob.glob(os.path.join(ROOT, "include", "*.h")))
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()
+
+
+def traffic_for(name: str):
+    """HBM bytes per launch of the workload's dominant kernel: calibrated
+    FETCH_SIZE + WRITE_SIZE from profiles/traffic_<name>.json, or None when
+    absent or measured on other kernel sources."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None, "not measured"
+    rec = json.load(open(path))
+    if rec.get("sources_sha256") != sources_sha256():
+        return None, "stale: measured on other kernel sources"
+    return rec.get("hbm_bytes_per_launch"), rec.get("measured")
 
 
 def context_lengths(cfg) -> list[int]:
@@ -105,7 +148,8 @@ def decode_workload(cfg, dev):
     return dict(ctx=ctx, bs=bs, k=k, v=v, q=q, table=table.to(dev),
                 ctx_dev=torch.tensor(ctx, dtype=torch.int32, device=dev),
                 table_host=table, algo_bytes=kv_bytes + qo_bytes + tbl_bytes,
-                flops=4 * sum(ctx) * cfg["hq"] * cfg["d"], dtype=dtype, scale=cfg["d"] ** -0.5)
+                flops=4 * sum(ctx) * cfg["hq"] * cfg["d"], dtype=dtype, eb=eb,
+                scale=cfg["d"] ** -0.5)
 
 
 def _event_us(ev, a: int, b: int):
@@ -117,33 +161,75 @@ def _event_us(ev, a: int, b: int):
     return sum(d) / n, med
 
 
-def cpu_baseline(cfg, w, budget_s: float):
+def time_steps(args, phases):
+    """Run W untimed steps, then K steps timed by wall clock (synchronised on
+    both sides), then K more steps with HIP events between the phases of each
+    step. ``phases``: callables run in order as one step; each takes the step
+    index. Returns (ms per step, [(mean us, median us) per phase])."""
+    import torch
+
+    def step(i):
+        for ph in phases:
+            ph(i)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    # HIP events on the stream the kernels run on. A leading device-side
+    # sleep keeps the GPU busy while every launch is queued, so host launch
+    # gaps stay out of the event intervals.
+    stream = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)]
+          for _ in range(args.steps)]
+    torch.cuda._sleep(50_000_000)
+    for i, e in enumerate(ev):
+        e[0].record(stream)
+        for j, ph in enumerate(phases):
+            ph(args.warmup + args.steps + i)
+            e[j + 1].record(stream)
+    torch.cuda.synchronize()
+    return ms, [_event_us(ev, j, j + 1) for j in range(len(phases))]
+
+
+def cpu_model() -> str:
+    name = platform.processor() or "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return name
+
+
+def cpu_threads() -> int:
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline_decode(host, budget_s: float):
     """The oracle's restatement of CpuAttentionBackend (fp32 upcast, grouped
-    einsum, softmax, einsum) over the batch's sequences on the host cores."""
+    einsum, softmax, einsum, output cast to the query dtype) over the batch's
+    sequences on the host cores: whole passes over the batch (one decode step
+    per sequence) until the budget is spent, at least one sequence."""
     import torch
     from oracle import attention as oa
 
-    threads = len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
-    bs = w["bs"]
-    kc, vc, q = w["k"].cpu(), w["v"].cpu(), w["q"].cpu()
-    seqs = []
-    for i, c in enumerate(w["ctx"]):
-        kk, vv = oa.gather_context(kc, vc, w["table_host"][i].tolist(), c)
-        seqs.append((q[i], kk.contiguous(), vv.contiguous()))
-    del kc, vc
-    # Whole passes over the batch (one decode step per sequence) until the
-    # budget is spent; a pass that would not fit the budget stops at the
-    # sequence where the budget runs out (at least one sequence).
-    eb = torch.finfo(w["dtype"]).bits // 8
+    seqs = host["seqs"]
+    eb = host["eb"]
     t0 = time.perf_counter()
-    passes, done, nbytes, tokens = 0, 0, 0, 0
+    passes, done, nbytes = 0, 0, 0
     while True:
         for qi, kk, vv in seqs:
-            oa.attend(qi, kk, vv, w["scale"]).to(w["dtype"])
+            oa.attend(qi, kk, vv, host["scale"]).to(host["dtype"])
             done += 1
             nbytes += kk.numel() * eb * 2 + qi.numel() * eb * 2
-            tokens += 1
             if time.perf_counter() - t0 > budget_s:
                 break
         else:
@@ -151,46 +237,98 @@ def cpu_baseline(cfg, w, budget_s: float):
             continue
         break
     dt = time.perf_counter() - t0
-    # One pass (or the part done above) with the reference's torch.cat append
-    # in front of each step.
+    # The sequences done above once more, each with the reference's
+    # torch.cat append in front of its step (src/core/attention_backend.py:105-110).
     t1 = time.perf_counter()
     cat_bytes = 0
-    for qi, kk, vv in seqs[:done]:
+    for qi, kk, vv in seqs[:min(done, len(seqs))]:
         k2 = torch.cat([kk, kk[-1:]], dim=0)
         v2 = torch.cat([vv, vv[-1:]], dim=0)
-        oa.attend(qi, k2, v2, w["scale"]).to(w["dtype"])
+        oa.attend(qi, k2, v2, host["scale"]).to(host["dtype"])
         cat_bytes += kk.numel() * eb * 2 + qi.numel() * eb * 2
     dt_cat = time.perf_counter() - t1
-    cpu_model = platform.processor() or "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {
-        "value": nbytes / dt / 1e9,
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{done} decode steps = {passes} whole passes over the {len(seqs)} sequences of the "
-                  f"same batch + {done - passes * len(seqs)} more, one step per sequence "
+        "value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": f"{done} decode steps = {passes} whole passes over the {len(seqs)} sequences of "
+                  f"the same batch + {done - passes * len(seqs)} more, one step per sequence "
                   f"(fp32 upcast + einsum + softmax + einsum, as CpuAttentionBackend.decode_layer)",
-        "seconds": dt,
-        "tokens_per_s": tokens / dt,
-        "with_cat_append_gbs": cat_bytes / dt_cat / 1e9,
-        "cpu_model": cpu_model,
+        "seconds": dt, "tokens_per_s": done / dt,
+        "with_cat_append_gbs": cat_bytes / dt_cat / 1e9 if dt_cat > 0 else None,
+        "cpu_model": cpu_model(),
     }
 
 
-def bench_decode(args, cfg):
+def cpu_baseline_prefill(host, budget_s: float):
+    """Chunked prefill on the host cores, two ways over the same sequences:
+    (1) successive append-then-attend decode steps (the oracle's
+    CpuAttentionBackend restatement, one query token at a time, as the
+    reference backend would serve a prompt), a bounded sample of tokens from
+    the start of each sequence's chunk; (2) the equivalent causal-masked fp32
+    contraction per kv head (one batched matmul form), whole sequences.
+    Both in TFLOP/s of causal-masked flops (4 D Hq per visible key)."""
+    import torch
+    from oracle import attention as oa
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    q, ks, vs, n_new, scale = host["q"], host["keys"], host["values"], host["new"], host["scale"]
+    hq, d = q.shape[2], q.shape[3]
+    S = q.shape[0]
+    # (1) successive decode steps: token i of every sequence in turn until
+    # half the budget is spent.
+    t0 = time.perf_counter()
+    flops, tokens = 0, 0
+    i = 0
+    while i < n_new and time.perf_counter() - t0 < budget_s / 2:
+        for s in range(S):
+            lim = ks[s].shape[0] - n_new + i + 1
+            oa.attend(q[s, i], ks[s][:lim], vs[s][:lim], scale).to(host["dtype"])
+            flops += 4 * d * hq * lim
+            tokens += 1
+        i += 1
+    dt_steps = time.perf_counter() - t0
+    # (2) the causal-masked contraction, whole sequences until the budget.
+    t1 = time.perf_counter()
+    mflops, mseqs = 0, 0
+    for s in range(S):
+        oa.chunked_prefill_masked(q[s], ks[s], vs[s], scale).to(host["dtype"])
+        L = ks[s].shape[0]
+        mflops += 4 * d * hq * sum(L - n_new + j + 1 for j in range(n_new))
+        mseqs += 1
+        if time.perf_counter() - t1 > budget_s / 2:
+            break
+    dt_masked = time.perf_counter() - t1
+    return {
+        "value": flops / dt_steps / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": f"{tokens} query tokens ({i} per sequence, from the start of each of the {S} "
+                  f"chunks) as successive append-then-attend decode steps (fp32 upcast + einsum "
+                  f"+ softmax + einsum, as CpuAttentionBackend.decode_layer)",
+        "seconds": dt_steps, "tokens_per_s": tokens / dt_steps,
+        "masked_contraction": {"value": mflops / dt_masked / 1e12, "unit": "TFLOP/s",
+                               "sample": f"{mseqs} whole sequences (512 query tokens each) as one "
+                                         f"causal-masked fp32 contraction per kv head",
+                               "seconds": dt_masked,
+                               "tokens_per_s": mseqs * n_new / dt_masked},
+        "cpu_model": cpu_model(),
+    }
+
+
+def roofline(bound: str, kernel: str, achieved: float, traffic, traffic_note):
+    peak = PEAK_HBM_GBS if bound == "hbm" else PEAK_BF16_TFLOPS
+    return {"bound": bound, "kernel": kernel, "achieved": achieved, "peak": peak,
+            "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": achieved / peak,
+            "traffic": traffic, "traffic_source": traffic_note}
+
+
+def measure_decode(args, name):
+    """One decode workload on the GPU: (entry, host data for the CPU baseline)."""
     import torch
     from cloverinfer_amd import kernels
 
+    cfg = DECODE_CONFIGS[name]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    log(f"building workload {args.config}")
+    log(f"{name}: building workload")
     w = decode_workload(cfg, dev)
     out = torch.empty_like(w["q"])
     max_ctx = max(w["ctx"])
@@ -203,22 +341,19 @@ def bench_decode(args, cfg):
     args_list = [kernels.decode_args(out, w["q"], kc, vc, w["table"], w["ctx_dev"], w["bs"],
                                      max_ctx, scale=w["scale"]) for kc, vc in pools]
     a = args_list[0]
+    waves = args.waves
     part = args.partition if args.partition is not None else cfg["partition"]
-    if part is not None and part < 0:  # explicit request for the automatic schedule
+    if part is not None and part < 0:
         part = None
     if part is None:
-        if kernels.balanced_supported(a):
-            mode = "balanced"
+        if waves > 0 and kernels.balanced_supported(a):
+            mode, part = "balanced", 0
         else:
-            hq, hkv = cfg["hq"], cfg["hkv"]
-            part = kernels.choose_partition(len(w["ctx"]), hkv, hq // hkv, max_ctx,
-                                            kernels.num_compute_units(dev))
-            mode = "split" if part > 0 and max_ctx > part else "single"
+            mode, part = kernels.choose_schedule(a, kernels.num_compute_units(dev))
     else:
         mode = "split" if part > 0 and max_ctx > part else "single"
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
     lib = kernels._native.load()
-    waves = args.waves
     if mode == "balanced":
         ws = kernels.splitk_workspace(dev, kernels.balanced_workspace_bytes(a, waves))
     elif mode == "split":
@@ -226,110 +361,214 @@ def bench_decode(args, cfg):
     else:
         ws = None
 
-    def first_half(i=0):
+    phases, names = [], []
+    append_bytes = 0
+    if cfg.get("append"):
+        # The step's append: token ctx - 1 of every sequence (its new row)
+        # through reshape_and_cache into the pool copy the step decodes.
+        g = torch.Generator(device=dev).manual_seed(cfg["seed"] + 7)
+        kn = torch.randn((len(w["ctx"]), cfg["hkv"], cfg["d"]), generator=g, device=dev).to(w["dtype"])
+        vn = torch.randn((len(w["ctx"]), cfg["hkv"], cfg["d"]), generator=g, device=dev).to(w["dtype"])
+        bs = w["bs"]
+        slots = torch.tensor([int(w["table_host"][s, (c - 1) // bs]) * bs + (c - 1) % bs
+                              for s, c in enumerate(w["ctx"])], dtype=torch.int64, device=dev)
+        append_bytes = 2 * kn.numel() * kn.element_size() * 2 + slots.numel() * 8
+
+        def append(i):
+            kc, vc = pools[i % copies]
+            kernels.reshape_and_cache(kn, vn, kc, vc, slots)
+
+        phases.append(append)
+        names.append("reshape_and_cache")
+
+    def first_half(i):
         a = args_list[i % copies]
         if mode == "balanced":
-            kernels.balanced_partials(a, waves, ws, stream.cuda_stream)
+            kernels.balanced_partials(a, waves, ws, stream)
         elif mode == "split":
-            kernels.paged_decode_partials(a, part, ws, stream.cuda_stream)
+            kernels.paged_decode_partials(a, part, ws, stream)
         else:
-            kernels._native.check(lib.clv_paged_decode(a, stream.cuda_stream), "clv_paged_decode")
+            kernels._native.check(lib.clv_paged_decode(a, stream), "clv_paged_decode")
 
-    def second_half(i=0):
+    def second_half(i):
         a = args_list[i % copies]
         if mode == "balanced":
-            kernels.balanced_reduce(a, waves, ws, stream.cuda_stream)
-        elif mode == "split":
-            kernels.splitk_reduce(a, part, ws, stream.cuda_stream)
+            kernels.balanced_reduce(a, waves, ws, stream)
+        else:
+            kernels.splitk_reduce(a, part, ws, stream)
 
-    def step(i=0):
-        first_half(i)
-        second_half(i)
-
-    log(f"warmup {args.warmup} (mode {mode}, partition {part if mode == 'split' else 0}, "
-        f"{copies} pool copies)")
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} steps")
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = wall / args.steps * 1e3
-
-    # Per-kernel durations: HIP events on the stream the kernels run on. A
-    # leading device-side sleep keeps the GPU busy while every launch is
-    # queued, so host launch gaps stay out of the event intervals.
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda._sleep(50_000_000)
-    for i, e in enumerate(ev):
-        e[0].record(stream)
-        first_half(i)
-        e[1].record(stream)
-        second_half(i)
-        e[2].record(stream)
-    torch.cuda.synchronize()
-    dec_us, dec_med = _event_us(ev, 0, 1)
-    red_us, red_med = _event_us(ev, 1, 2)
-    log(f"step {ms:.4f} ms, decode kernel {dec_us:.1f} us, reduce {red_us:.1f} us")
-
-    value = w["algo_bytes"] / (ms * 1e-3) / 1e9
-    achieved = w["algo_bytes"] / (dec_us * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                         f"traffic_{args.config}.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
-    result = {
-        "metric": METRIC,
-        "value": value,
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+    phases.append(first_half)
+    names.append("paged_decode")
+    if mode != "single":
+        phases.append(second_half)
+        names.append("merge")
+    log(f"{name}: warmup {args.warmup}, {args.steps} steps (schedule {mode}, partition "
+        f"{part if mode == 'split' else 0}, {copies} pool copies)")
+    ms, ev = time_steps(args, phases)
+    dec_us = ev[names.index("paged_decode")][0]
+    log(f"{name}: step {ms:.4f} ms, " + ", ".join(f"{n} {e[0]:.1f} us" for n, e in zip(names, ev)))
+    step_bytes = w["algo_bytes"] + append_bytes
+    kernel = {"balanced": "paged_decode_stream", "split": "paged_decode_mfma (split-K partials)",
+              "single": "paged_decode_mfma (single pass)"}[mode]
+    traffic, note = traffic_for(name)
+    entry = {
+        "workload": cfg["workload"],
+        "value": step_bytes / (ms * 1e-3) / 1e9, "unit": "GB/s",
         "ms_per_step": ms,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}[cfg["dtype"]],
-        "data": "synthetic N(0,1) q/K/V, random init, seeded; no model weights",
-        "config": {
-            "workload": cfg["workload"],
-            "num_seqs": len(w["ctx"]),
-            "num_heads": cfg["hq"],
-            "num_kv_heads": cfg["hkv"],
-            "head_dim": cfg["d"],
-            "block_size": w["bs"],
-            "total_context_tokens": sum(w["ctx"]),
-            "max_context_len": max_ctx,
-            "schedule": mode,
-            "partition_size": part if mode == "split" else 0,
-            "kv_pool_copies": copies,
-            "algorithmic_bytes_per_step": w["algo_bytes"],
-            "seed": cfg["seed"],
-        },
         "tokens_per_s": len(w["ctx"]) / (ms * 1e-3),
-        "hbm_frac_of_peak": value / PEAK_HBM_GBS,
-        "kernels_us": {"paged_decode": dec_us, "merge": red_us},
-        "kernels_us_median": {"paged_decode": dec_med, "merge": red_med},
-        "roofline": {
-            "bound": "hbm",
-            "kernel": {"balanced": "paged_decode_stream", "split": "paged_decode_mfma",
-                       "single": "paged_decode_mfma"}[mode] if cfg["d"] in (64, 128)
-                      else "paged_decode_valu",
-            "achieved": achieved,
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": achieved / PEAK_HBM_GBS,
-            "traffic": traffic,
-        },
+        "dtype": DTYPE_TAG[cfg["dtype"]],
+        "num_seqs": len(w["ctx"]), "num_heads": cfg["hq"], "num_kv_heads": cfg["hkv"],
+        "head_dim": cfg["d"], "block_size": w["bs"],
+        "total_context_tokens": sum(w["ctx"]), "max_context_len": max_ctx,
+        "schedule": mode, "partition_size": part if mode == "split" else 0,
+        "kv_pool_copies": copies, "seed": cfg["seed"],
+        "algorithmic_bytes_per_step": step_bytes,
+        "decode_algorithmic_bytes": w["algo_bytes"],
+        "kernels_us": {n: e[0] for n, e in zip(names, ev)},
+        "kernels_us_median": {n: e[1] for n, e in zip(names, ev)},
+        "roofline": roofline("hbm", kernel, w["algo_bytes"] / (dec_us * 1e-6) / 1e9, traffic, note),
     }
+    # Host copies for the CPU baseline: each sequence's context gathered into
+    # the reference backend's contiguous [L, Hkv, D] form (untimed setup).
+    from oracle import attention as oa
+
+    kc, vc, q = w["k"].cpu(), w["v"].cpu(), w["q"].cpu()
+    seqs = []
+    for i, c in enumerate(w["ctx"]):
+        kk, vv = oa.gather_context(kc, vc, w["table_host"][i].tolist(), c)
+        seqs.append((q[i], kk.contiguous(), vv.contiguous()))
+    host = {"seqs": seqs, "eb": w["eb"], "dtype": w["dtype"], "scale": w["scale"]}
+    del pools, args_list, w
+    torch.cuda.empty_cache()
+    return entry, host
+
+
+def measure_prefill(args):
+    """Chunked prefill, 8 sequences x (4096 cached + 512 new), 32 q / 8 kv
+    heads, head_dim 128, bf16: a step appends the 512 new K/V rows of every
+    sequence (reshape_and_cache) and runs the causal chunk attention."""
+    import torch
+    from cloverinfer_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    S, cached, new, hq, hkv, d, bs = 8, 4096, 512, 32, 8, 128, 16
+    seed = 1005
+    log("prefill: building workload")
+    ctx = [cached + new] * S
+    need = [math.ceil(c / bs) for c in ctx]
+    nb = sum(need)
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(nb, generator=g)
+    table_host = perm.view(S, -1).to(torch.int32)
+    table = table_host.to(dev)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    v = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    q = torch.randn((S * new, hq, d), generator=gd, device=dev).to(torch.bfloat16)
+    kn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    vn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
+    pos = torch.arange(cached, cached + new)
+    slots = torch.cat([table_host[s].long()[pos // bs] * bs + pos % bs for s in range(S)]).to(dev)
+    ctx_dev = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    qsl = torch.arange(0, S * new + 1, new, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    scale = d ** -0.5
+
+    def append(i):
+        kernels.reshape_and_cache(kn, vn, k, v, slots)
+
+    def attend(i):
+        kernels.chunked_prefill(out, q, k, v, table, ctx_dev, qsl, new, scale=scale)
+
+    log(f"prefill: warmup {args.warmup}, {args.steps} steps")
+    ms, ev = time_steps(args, [append, attend])
+    (app_us, app_med), (att_us, att_med) = ev
+    log(f"prefill: step {ms:.4f} ms, append {app_us:.1f} us, prefill {att_us:.1f} us")
+    flops = 4 * d * hq * S * sum(cached + i + 1 for i in range(new))
+    traffic, note = traffic_for("prefill")
+    entry = {
+        "workload": "chunked prefill: 8 seqs x (4096 cached + 512 new), 32 q / 8 kv heads, "
+                    "head_dim 128, block 16, bf16, causal in chunk; a step appends the 4096 new "
+                    "K/V rows (reshape_and_cache) and runs the prefill",
+        "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+        "ms_per_step": ms,
+        "tokens_per_s": S * new / (ms * 1e-3),
+        "dtype": "bf16", "seed": seed,
+        "flops_per_step": flops,
+        "kernels_us": {"reshape_and_cache": app_us, "chunked_prefill": att_us},
+        "kernels_us_median": {"reshape_and_cache": app_med, "chunked_prefill": att_med},
+        "roofline": roofline("mfma", "chunked_prefill_mfma", flops / (att_us * 1e-6) / 1e12,
+                             traffic, note),
+    }
+    # Host copies for the CPU baseline: each sequence's whole context in the
+    # reference backend's contiguous form, the query rows per sequence.
+    from oracle import attention as oa
+
+    kc, vc = k.cpu(), v.cpu()
+    keys, values = [], []
+    for s in range(S):
+        kk, vv = oa.gather_context(kc, vc, table_host[s].tolist(), ctx[s])
+        keys.append(kk.contiguous())
+        values.append(vv.contiguous())
+    host = {"q": q.cpu().view(S, new, hq, d), "keys": keys, "values": values, "new": new,
+            "scale": scale, "dtype": torch.bfloat16}
+    del k, v, q, kn, vn, out
+    torch.cuda.empty_cache()
+    return entry, host
+
+
+def bench_all(args, names):
+    measured = {}
+    for name in names:
+        if name == "prefill":
+            measured[name] = measure_prefill(args)
+        else:
+            measured[name] = measure_decode(args, name)
     if not args.no_cpu:
-        log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(cfg, w, args.cpu_budget)
-    return result
+        for name in names:
+            log(f"{name}: cpu baseline")
+            entry, host = measured[name]
+            budget = args.cpu_budget if args.cpu_budget > 0 else CPU_BUDGET_S.get(name, 10.0)
+            if name == "prefill":
+                entry["cpu_baseline"] = cpu_baseline_prefill(host, budget)
+            else:
+                entry["cpu_baseline"] = cpu_baseline_decode(host, budget)
+    return {n: measured[n][0] for n in names}
+
+
+def result_line(args, entries, head: str):
+    """The contract's JSON object: the headline workload's fields at the top,
+    every measured workload under "configs"."""
+    e = entries[head]
+    is_prefill = head == "prefill"
+    metric = ("chunked-prefill MFMA TFLOP/s (causal-masked flops)" if is_prefill else
+              METRIC if head == "qwen7b" else f"decode-attn HBM GB/s, {head} workload, 1 GPU")
+    res = {
+        "metric": metric,
+        "value": e["value"], "unit": e["unit"], "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": e["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": e["dtype"],
+        "data": "synthetic N(0,1) q/K/V (x0.5 for the Llama-7B shape), random init, seeded; "
+                "no model weights",
+        "config": {k: v for k, v in e.items()
+                   if k not in ("value", "unit", "ms_per_step", "dtype", "kernels_us",
+                                "kernels_us_median", "roofline", "cpu_baseline",
+                                "tokens_per_s")},
+        "tokens_per_s": e["tokens_per_s"],
+        "kernels_us": e["kernels_us"],
+        "kernels_us_median": e["kernels_us_median"],
+        "roofline": e["roofline"],
+    }
+    if not is_prefill:
+        res["hbm_frac_of_peak"] = e["value"] / PEAK_HBM_GBS
+    if "cpu_baseline" in e:
+        res["cpu_baseline"] = e["cpu_baseline"]
+    if len(entries) > 1:
+        res["configs"] = entries
+    res["sources_sha256"] = sources_sha256()[:16]
+    return res
 
 
 def bench_decode_fp8(args):
@@ -358,33 +597,20 @@ def bench_decode_fp8(args):
     waves = args.waves or lib.clv_default_num_waves_fp8()
     ws = kernels.splitk_workspace(dev, kernels.balanced_workspace_bytes(a, waves))
 
-    def step():
+    def step(i):
         kernels._native.check(lib.clv_paged_decode_fp8(a, ones.data_ptr(), ones.data_ptr(),
                                                        waves, ws.data_ptr(), ws.numel(),
                                                        stream.cuda_stream), "clv_paged_decode_fp8")
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-    torch.cuda._sleep(50_000_000)
-    for e in ev:
-        e[0].record(stream)
-        step()
-        e[1].record(stream)
-    torch.cuda.synchronize()
-    call_us, call_med = _event_us(ev, 0, 1)
+    ms, ev = time_steps(args, [step])
+    call_us, call_med = ev[0]
     ctx = w["ctx"]
     kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * 1 * 2
     qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * 2 * 2
     tbl_bytes = sum(math.ceil(c / w["bs"]) for c in ctx) * 4 + len(ctx) * 4
     algo = kv_bytes + qo_bytes + tbl_bytes
     log(f"step {ms:.4f} ms, decode + merge {call_us:.1f} us")
+    traffic, note = traffic_for("qwen7b_fp8")
     return {
         "metric": "decode-attn HBM GB/s, fp8 KV pools, GQA-7B shape, 1 GPU",
         "value": algo / (ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -399,112 +625,28 @@ def bench_decode_fp8(args):
         "tokens_per_s": len(ctx) / (ms * 1e-3),
         "kernels_us": {"paged_decode_fp8_with_merge": call_us},
         "kernels_us_median": {"paged_decode_fp8_with_merge": call_med},
-        "roofline": {"bound": "hbm", "kernel": "paged_decode_stream (fp8) + merge",
-                     "achieved": algo / (call_us * 1e-6) / 1e9, "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": algo / (call_us * 1e-6) / 1e9 / PEAK_HBM_GBS,
-                     "traffic": None},
-    }
-
-
-def bench_prefill(args):
-    """Chunked prefill, 8 sequences x (4096 cached + 512 new), 32 q / 8 kv
-    heads, head_dim 128, bf16: a step appends the 512 new K/V rows of every
-    sequence (reshape_and_cache) and runs the causal chunk attention."""
-    import torch
-    from cloverinfer_amd import kernels
-
-    dev = torch.device("cuda", 0)
-    S, cached, new, hq, hkv, d, bs = 8, 4096, 512, 32, 8, 128, 16
-    seed = 1005
-    ctx = [cached + new] * S
-    need = [math.ceil(c / bs) for c in ctx]
-    nb = sum(need)
-    g = torch.Generator().manual_seed(seed)
-    perm = torch.randperm(nb, generator=g)
-    table = perm.view(S, -1).to(torch.int32).to(dev)
-    gd = torch.Generator(device=dev).manual_seed(seed)
-    k = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
-    v = torch.randn((nb, bs, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
-    q = torch.randn((S * new, hq, d), generator=gd, device=dev).to(torch.bfloat16)
-    kn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
-    vn = torch.randn((S * new, hkv, d), generator=gd, device=dev).to(torch.bfloat16)
-    pos = torch.arange(cached, cached + new)
-    slots = torch.cat([table[s].long().cpu()[pos // bs] * bs + pos % bs for s in range(S)]).to(dev)
-    ctx_dev = torch.tensor(ctx, dtype=torch.int32, device=dev)
-    qsl = torch.arange(0, S * new + 1, new, dtype=torch.int32, device=dev)
-    out = torch.empty_like(q)
-    scale = d ** -0.5
-
-    def append():
-        kernels.reshape_and_cache(kn, vn, k, v, slots)
-
-    def attend():
-        kernels.chunked_prefill(out, q, k, v, table, ctx_dev, qsl, new, scale=scale)
-
-    for _ in range(args.warmup):
-        append()
-        attend()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        append()
-        attend()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
-    stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    for e in ev:
-        e[0].record(stream)
-        append()
-        e[1].record(stream)
-        attend()
-        e[2].record(stream)
-    torch.cuda.synchronize()
-    app_us, app_med = _event_us(ev, 0, 1)
-    att_us, att_med = _event_us(ev, 1, 2)
-    flops = 4 * d * hq * S * sum(cached + i + 1 for i in range(new))
-    achieved = flops / (att_us * 1e-6) / 1e12
-    return {
-        "metric": "chunked-prefill MFMA TFLOP/s (causal-masked flops)",
-        "value": flops / (ms * 1e-3) / 1e12,
-        "unit": "TFLOP/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic N(0,1), seeded",
-        "config": {"workload": "chunked prefill: 8 seqs x (4096 cached + 512 new), 32 q / 8 kv "
-                               "heads, head_dim 128, block 16, bf16, causal in chunk",
-                   "flops_per_step": flops},
-        "tokens_per_s": S * new / (ms * 1e-3),
-        "kernels_us": {"reshape_and_cache": app_us, "chunked_prefill": att_us},
-        "kernels_us_median": {"reshape_and_cache": app_med, "chunked_prefill": att_med},
-        "roofline": {"bound": "mfma", "kernel": "chunked_prefill", "achieved": achieved,
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None},
+        "roofline": roofline("hbm", "paged_decode_stream (fp8) + merge",
+                             algo / (call_us * 1e-6) / 1e9, traffic, note),
     }
 
 
 def bench_copy(args):
     """Calibration workload: a plain device copy of a known number of bytes
-    (2 GiB read + 2 GiB written per step), used to scale HBM byte counters."""
+    (``--copy-mib`` MiB read + the same written per step), used to scale HBM
+    byte counters."""
     import torch
 
     dev = torch.device("cuda", 0)
-    n = 1 << 31
+    n = args.copy_mib << 20
     src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    for _ in range(args.warmup):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    ms, _ = time_steps(args, [lambda i: dst.copy_(src)])
     return {"metric": "device copy GB/s (read + write)", "value": 2 * n / (ms * 1e-3) / 1e9,
             "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "u8", "data": "constant bytes",
-            "config": {"workload": "calibration copy, 2 GiB read + 2 GiB write per step",
+            "config": {"workload": f"calibration copy, {args.copy_mib} MiB read + "
+                                   f"{args.copy_mib} MiB written per step",
                        "bytes_read_per_step": n, "bytes_written_per_step": n}}
 
 
@@ -569,20 +711,21 @@ def bench_node(args, dtype_name="bfloat16", packed=False):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # The GPU clock ramps up over the first tens of milliseconds of a run:
-    # 200 untimed steps (about 40 ms of decode) reach the steady clock.
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", default="qwen7b",
-                    choices=sorted(DECODE_CONFIGS) + ["qwen7b_fp8", "prefill", "copy", "node",
-                                                      "node_fp32", "node_packed"])
+    # The GPU clock ramps up over the first tens of milliseconds of a run.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", default="all",
+                    choices=["all"] + sorted(DECODE_CONFIGS) +
+                            ["qwen7b_fp8", "prefill", "copy", "node", "node_fp32", "node_packed"])
     ap.add_argument("--partition", type=int, default=None,
                     help="split-K partition size (0 = single pass, -1 or default: automatic)")
     ap.add_argument("--waves", type=int, default=0,
                     help="waves of the balanced decode (0 = device default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-budget", type=float, default=15.0,
-                    help="seconds of CPU baseline work (a bounded sample)")
+    ap.add_argument("--cpu-budget", type=float, default=0.0,
+                    help="seconds of CPU baseline work per workload (0: the built-in "
+                         "per-workload budgets, 5-10 s)")
+    ap.add_argument("--copy-mib", type=int, default=2048, help="size of the calibration copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the paged-attention "
@@ -594,20 +737,20 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
-    if args.config == "qwen7b_fp8":
+    if args.config == "all":
+        result = result_line(args, bench_all(args, ALL), "qwen7b")
+    elif args.config in DECODE_CONFIGS or args.config == "prefill":
+        result = result_line(args, bench_all(args, [args.config]), args.config)
+    elif args.config == "qwen7b_fp8":
         result = bench_decode_fp8(args)
-    elif args.config == "prefill":
-        result = bench_prefill(args)
     elif args.config == "copy":
         result = bench_copy(args)
     elif args.config == "node":
         result = bench_node(args)
     elif args.config == "node_fp32":
         result = bench_node(args, "float32")
-    elif args.config == "node_packed":
-        result = bench_node(args, packed=True)
     else:
-        result = bench_decode(args, DECODE_CONFIGS[args.config])
+        result = bench_node(args, packed=True)
     print(json.dumps(result), flush=True)
     return 0
 

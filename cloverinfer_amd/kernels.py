@@ -196,6 +196,25 @@ def balanced_supported(a: _native.DecodeArgs) -> bool:
             and a.head_dim in (64, 128) and a.block_size >= 4 and nseg <= BALANCED_MAX_SEGMENTS)
 
 
+def choose_schedule(a: _native.DecodeArgs, num_cus: int) -> tuple[str, int]:
+    """Decode schedule for a batch: ("single", 0), ("balanced", 0) or
+    ("split", partition_size).
+
+    Contexts of at most DEFAULT_PARTITION tokens take the single pass (one
+    workgroup per (sequence, kv head, 16 query heads), no merge): its longest
+    workgroup is short, so the load imbalance the balanced schedule removes
+    costs less than the balanced schedule's merge launch. Longer contexts
+    take the balanced stream decode where it applies, else split-K or the
+    single pass by :func:`choose_partition`."""
+    if a.max_context_len <= DEFAULT_PARTITION:
+        return "single", 0
+    if balanced_supported(a):
+        return "balanced", 0
+    part = choose_partition(a.num_seqs, a.num_kv_heads, a.num_heads // a.num_kv_heads,
+                            a.max_context_len, num_cus)
+    return ("split", part) if part > 0 and a.max_context_len > part else ("single", 0)
+
+
 def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_tables: torch.Tensor,
                     context_lens: torch.Tensor, block_size: int, max_context_len: int,
@@ -206,10 +225,12 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     Same arguments as the reference op (src/kernels/csrc/manager.cpp:19-27);
     ``scale`` defaults to 1/sqrt(head_dim) as in src/kernels/csrc/attention.cu:60.
     GQA follows from ``k_cache.shape[2] < q.shape[1]``. ``partition_size``:
-    None picks the schedule (the balanced stream decode where it applies,
-    with ``num_waves`` waves, 0 = the device default), 0 forces a single
-    pass per (sequence, kv head), a positive multiple of 32 forces split-K
-    with that many tokens per partition.
+    None picks the schedule (:func:`choose_schedule`: the single pass for
+    contexts up to 512 tokens, else the balanced stream decode where it
+    applies; a positive ``num_waves`` asks for the balanced decode with that
+    many waves, 0 = the device default), 0 forces a single pass per
+    (sequence, kv head), a positive multiple of 32 forces split-K with that
+    many tokens per partition.
 
     fp8 pools (``k_cache.dtype == FP8``): K = e4m3 * ``k_scale``, V = e4m3 *
     ``v_scale`` (numbers or per-kv-head values), balanced schedule only
@@ -234,16 +255,17 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                       "clv_paged_decode_fp8")
         return
     if partition_size is None:
-        if balanced_supported(a):
+        if num_waves > 0 and balanced_supported(a):
+            mode = "balanced"  # an explicit wave count asks for the balanced schedule
+        else:
+            mode, partition_size = choose_schedule(a, num_compute_units(dev))
+        if mode == "balanced":
             nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
                                                       a.head_dim, num_waves)
             ws = splitk_workspace(dev, nbytes)
             _native.check(lib.clv_paged_decode_balanced(a, num_waves, ws.data_ptr(), ws.numel(),
                                                         stream), "clv_paged_decode_balanced")
             return
-        partition_size = choose_partition(a.num_seqs, a.num_kv_heads,
-                                          a.num_heads // a.num_kv_heads, a.max_context_len,
-                                          num_compute_units(dev))
     if partition_size == 0 or a.max_context_len <= partition_size:
         _native.check(lib.clv_paged_decode(a, stream), "clv_paged_decode")
         return

@@ -187,6 +187,29 @@ def chunked_prefill(q_new: torch.Tensor, keys: torch.Tensor, values: torch.Tenso
     return out
 
 
+def chunked_prefill_masked(q_new: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+                           score_scale: float) -> torch.Tensor:
+    """Same result as :func:`chunked_prefill` as one causal-masked fp32
+    contraction per kv head (scores ``[G*n, L]``, key ``j`` visible to query
+    row ``i`` iff ``j <= L - n + i``, softmax, times V): the dense
+    formulation of the n successive append-then-attend steps of
+    src/core/attention_backend.py:105-118, with the GQA grouping of
+    src/core/model_adapter.py:506-507 (query head h reads kv head h // G)."""
+    n, hq, d = q_new.shape
+    length, hkv, _ = keys.shape
+    g = hq // hkv
+    lim = length - n + torch.arange(n)                     # last visible key per row
+    visible = torch.arange(length)[None, :] <= lim[:, None]  # [n, L]
+    qf = q_new.float().reshape(n, hkv, g, d).permute(1, 0, 2, 3).reshape(hkv, n * g, d)
+    kf = keys.float().permute(1, 2, 0)                      # [Hkv, D, L]
+    vf = values.float().permute(1, 0, 2)                    # [Hkv, L, D]
+    scores = torch.bmm(qf, kf) * float(score_scale)         # [Hkv, n*G, L]
+    mask = visible.repeat_interleave(g, dim=0)              # row r is token r // G
+    scores = scores.masked_fill(~mask[None], float("-inf"))
+    ctx = torch.bmm(torch.softmax(scores, dim=-1), vf)      # [Hkv, n*G, D]
+    return ctx.reshape(hkv, n, g, d).permute(1, 0, 2, 3).reshape(n, hq, d)
+
+
 def brute_attention_fp64(q: np.ndarray, keys: np.ndarray, values: np.ndarray,
                          score_scale: float) -> np.ndarray:
     """Explicit-loop float64 attention for tiny shapes (an independent

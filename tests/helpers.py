@@ -73,3 +73,46 @@ def padded_tables(tables, width: int | None = None) -> torch.Tensor:
     for i, t in enumerate(tables):
         out[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
     return out
+
+
+# The literal bar of the hot path's parity requirement, for the five
+# benchmark workloads: max-abs 2e-3 against the fp32 oracle everywhere, and
+# max-rel 1e-2 where |ref| >= 0.2 (a relative bound on near-zero outputs is
+# ill-posed: a 16-bit output of 1e-4 is rounded by more than 1 % of itself).
+NS_ATOL = 2e-3
+NS_RTOL = 1e-2
+NS_REL_FLOOR = 0.2
+
+
+def assert_north_star_bar(got: torch.Tensor, ref: torch.Tensor, what: str) -> dict:
+    """Assert max-abs <= 2e-3 and max-rel <= 1e-2 (where |ref| >= 0.2);
+    print the observed margins and, when CLV_PARITY_LOG names a file, append
+    them to it as a JSON line. Returns the figures."""
+    import json
+    import os
+
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} != {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{what}: non-finite output"
+    err = (got - ref).abs()
+    big = ref.abs() >= NS_REL_FLOOR
+    rec = {
+        "what": what,
+        "elements": err.numel(),
+        "max_abs": err.max().item(),
+        "mean_abs": err.mean().item(),
+        "max_rel": (err[big] / ref.abs()[big]).max().item() if big.any() else 0.0,
+        "rel_elements": int(big.sum()),
+        "max_abs_ref": ref.abs().max().item(),
+    }
+    print(f"[parity] {what}: max-abs {rec['max_abs']:.3e} (bar {NS_ATOL:g}), max-rel "
+          f"{rec['max_rel']:.3e} over {rec['rel_elements']} elements with |ref| >= "
+          f"{NS_REL_FLOOR:g} (bar {NS_RTOL:g}); max |ref| {rec['max_abs_ref']:.3f}", flush=True)
+    path = os.environ.get("CLV_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    assert rec["max_abs"] <= NS_ATOL, f"{what}: max-abs {rec['max_abs']:.3e} > {NS_ATOL:g}"
+    assert rec["max_rel"] <= NS_RTOL, f"{what}: max-rel {rec['max_rel']:.3e} > {NS_RTOL:g}"
+    return rec

@@ -62,7 +62,9 @@ def test_fused_append_decode(hq, hkv, d, bs, dtype):
                  for t, c in zip(tables, grow)]
         kernels.reshape_and_cache(kn, vn, ku, vu, torch.tensor(slots, dtype=torch.int64, device=DEV))
         out_u = torch.empty_like(q)
-        kernels.paged_attention(out_u, q, ku, vu, bt, lens, bs, max(grow), scale=scale)
+        # the balanced schedule with the fused call's (default) wave count
+        kernels.paged_attention(out_u, q, ku, vu, bt, lens, bs, max(grow), scale=scale,
+                                num_waves=kernels._native.load().clv_default_num_waves())
         torch.cuda.synchronize()
         assert _same_bits(kf, ku) and _same_bits(vf, vu), f"pools differ at step {step}"
         assert torch.equal(out_f, out_u), f"fused output differs from the two-call form, step {step}"

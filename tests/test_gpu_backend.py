@@ -318,11 +318,15 @@ def test_malformed_payload_leaves_state_unchanged():
                 ("query", torch.randn(1, hq + 1, d).to(dtype))):
         with pytest.raises((ValueError, RuntimeError)):
             gpu.decode_layer_batch(items(bad))
+        packed = {"query": torch.randn(len(rids), hq, d).to(dtype),
+                  "key": torch.randn(len(rids), hkv, d).to(dtype),
+                  "value": torch.randn(len(rids), hkv, d).to(dtype)}
+        packed[bad[0]] = {"key": torch.randn(len(rids), hkv + 1, d),
+                          "value": torch.randn(len(rids), hkv, d - 8),
+                          "query": torch.randn(len(rids), hq + 1, d)}[bad[0]].to(dtype)
         with pytest.raises((ValueError, RuntimeError)):
-            q = torch.randn(len(rids), hq, d).to(dtype)
-            k = torch.randn(len(rids), hkv, d).to(dtype)
-            gpu.decode_layer_packed(rids, 0, q, k[:, :1] if bad[0] != "query" else k,
-                                    k if bad[0] != "query" else k, 0.125)
+            gpu.decode_layer_packed(rids, 0, packed["query"], packed["key"], packed["value"],
+                                    0.125)
     assert len(gpu.free_blocks) == free0
     assert [gpu.get_context_len(r) for r in rids] == lens
     for step in range(3):

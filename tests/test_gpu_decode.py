@@ -10,7 +10,8 @@ import torch
 from cloverinfer_amd import kernels
 from cloverinfer_amd.memory_manager import KVCacheManager
 from oracle import attention as oa
-from tests.helpers import assert_attention_close, make_paged_kv, padded_tables
+from tests.helpers import (assert_attention_close, assert_north_star_bar, make_paged_kv,
+                           padded_tables)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -98,12 +99,13 @@ def test_fp32_balanced_decode_is_fp32_exact(d, bs):
 
 def test_balanced_decode_many_segments():
     """4096 (sequence, kv head) segments: the largest count the balanced
-    decode holds; one more sequence falls back to the split-K schedule."""
+    decode holds (asked for by a wave count); one more sequence falls back to
+    the schedule chosen without it."""
     for nseq in (1024, 1025):
         ctx = [int(x) for x in torch.randint(0, 70, (nseq,),
                                               generator=torch.Generator().manual_seed(nseq))]
         q, k, v, tables, scale = case(nseq, ctx, 8, 4, 64, 16, torch.float16)
-        got = run_decode(q, k, v, tables, ctx, scale)
+        got = run_decode(q, k, v, tables, ctx, scale, num_waves=1024)
         ref = oa.paged_decode(q, k, v, tables, ctx, scale)
         assert_attention_close(got, ref, what=f"{nseq} seqs")
 
@@ -225,9 +227,10 @@ def test_config_opt125m_fp32_with_append():
     torch.cuda.synchronize()
     ref = torch.stack([oa.attend(q[i], kv[r][0], kv[r][1], 1 / 8) for i, r in enumerate(rids)])
     assert_attention_close(out.cpu(), ref, atol=1e-4, rtol=1e-4)
+    assert_north_star_bar(out, ref, "opt125m fp32, 8 x 128 (full config)")
 
 
-@pytest.mark.parametrize("nseq", [4])
+@pytest.mark.parametrize("nseq", [8])
 def test_config_llama7b_mha_fp16(nseq):
     ctx = [2048] * nseq
     q, k, v, tables, scale = case(1002, ctx, 32, 32, 128, 16, torch.float16, value_scale=0.5)
@@ -235,18 +238,21 @@ def test_config_llama7b_mha_fp16(nseq):
     for partition in (None, 0, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"llama7b P{partition}")
+        assert_north_star_bar(got, ref, f"llama7b fp16, {nseq} x 2048, partition {partition}")
 
 
 def test_config_qwen7b_gqa_bf16_ragged():
     ctx = [int(torch.randint(256, 8193, (1,), generator=torch.Generator().manual_seed(1003000 + i)))
-           for i in range(8)]
+           for i in range(16)]
     q, k, v, tables, scale = case(1003, ctx, 28, 4, 128, 16, torch.bfloat16)
     ref = oa.paged_decode(q, k, v, tables, ctx, scale)
     for partition in (None, 0, 256, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"qwen7b P{partition}")
+        assert_north_star_bar(got, ref, f"qwen7b bf16, 16 seqs U[256,8192], partition {partition}")
     got = run_decode(q, k, v, tables, ctx, scale, num_waves=37)
     assert_attention_close(got, ref, what="qwen7b balanced W=37")
+    assert_north_star_bar(got, ref, "qwen7b bf16, 16 seqs, balanced W=37")
 
 
 def test_config_long_context_splitk_fp16():
@@ -256,3 +262,4 @@ def test_config_long_context_splitk_fp16():
     for partition in (512, None):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"long-context P{partition}")
+        assert_north_star_bar(got, ref, f"long32k fp16, 2 x 32768, partition {partition}")

@@ -9,7 +9,8 @@ import torch
 
 from cloverinfer_amd import kernels
 from oracle import attention as oa
-from tests.helpers import assert_attention_close, make_paged_kv, padded_tables
+from tests.helpers import (assert_attention_close, assert_north_star_bar, make_paged_kv,
+                           padded_tables)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -66,6 +67,24 @@ def test_prefill_reduced_chunk_config():
     got = run_prefill(q, k, v, tables, ctx, qsl, scale)
     ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
     assert_attention_close(got, ref, what="chunked prefill 4096+512")
+    assert_north_star_bar(got, ref, "prefill bf16, 2 x (4096 + 512), successive-step oracle")
+
+
+def test_prefill_full_config_against_masked_oracle():
+    """All 8 sequences of the chunked-prefill config (4096 cached + 512 new,
+    32 q / 8 kv heads, bf16) against the oracle's causal-masked contraction
+    (pinned against the successive decode steps and float64 brute force)."""
+    cached, new = [4096] * 8, [512] * 8
+    q, k, v, tables, ctx, qsl = build(1005, cached, new, 32, 8, 128, 16, torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    refs = []
+    for s in range(8):
+        kk, vv = oa.gather_context(k, v, tables[s], ctx[s])
+        refs.append(oa.chunked_prefill_masked(q[qsl[s]:qsl[s + 1]], kk, vv, scale))
+    ref = torch.cat(refs)
+    assert_attention_close(got, ref, what="chunked prefill 8 x (4096+512)")
+    assert_north_star_bar(got, ref, "prefill bf16, 8 x (4096 + 512) (full config)")
 
 
 def test_prefill_rows_equal_decode_steps_full_config():

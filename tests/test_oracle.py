@@ -154,6 +154,25 @@ def test_chunked_prefill_equals_successive_decode_steps():
     assert cpu.get_context_len("r") == cached + new
 
 
+@pytest.mark.parametrize("cached,new,hkv,G,d", [(11, 6, 2, 2, 8), (0, 5, 1, 3, 4), (30, 1, 2, 1, 16)])
+def test_masked_prefill_equals_successive_steps_and_fp64(cached, new, hkv, G, d):
+    """The dense causal-masked formulation (the CPU baseline of chunked
+    prefill) equals the successive decode steps and, row by row, the float64
+    brute force over exactly the visible keys: a mask off by one (a row seeing
+    its successor's key, or not its own) or a wrong head regrouping fails."""
+    g = torch.Generator().manual_seed(cached + new)
+    k = torch.randn(cached + new, hkv, d, generator=g)
+    v = torch.randn(cached + new, hkv, d, generator=g)
+    q = torch.randn(new, hkv * G, d, generator=g)
+    dense = oa.chunked_prefill_masked(q, k, v, 0.3)
+    assert torch.allclose(dense, oa.chunked_prefill(q, k, v, 0.3), atol=1e-5)
+    for i in range(new):
+        lim = cached + i + 1
+        ref = oa.brute_attention_fp64(q[i].double().numpy(), k[:lim].double().numpy(),
+                                      v[:lim].double().numpy(), 0.3)
+        assert np.allclose(dense[i].double().numpy(), ref, atol=1e-5)
+
+
 def test_cpu_oracle_protocol_semantics():
     cpu = oa.CpuAttentionOracle()
     kv = [{"key": torch.randn(3, 2, 4), "value": torch.randn(3, 2, 4)} for _ in range(2)]

@@ -509,12 +509,28 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       for (int m = 0; m < CH; ++m) dst[16 * m] = (T)(o[rt][m][e] * inv);
     }
   }
+
+  // Rows past the grid's query tiles (a chunk longer than max_query_len, a
+  // caller error) are filled with NaN by the workgroup of the last tile, so
+  // that the error shows in the output instead of stale memory.
+  if (qt == n_qtiles - 1 && q_hi < n_new) {
+    const T nan = (T)__builtin_nanf("");
+    for (int idx = tid; idx < (n_new - q_hi) * G * D; idx += kThreads) {
+      const int d = idx % D;
+      const int h = (idx / D) % G;
+      const int tok = q_hi + idx / (D * G);
+      ((T *)p.out)[(int64_t)(qs + tok) * p.out_stride_token +
+                   (int64_t)(kvh * G + h) * p.out_stride_head + d] = nan;
+    }
+  }
 }
 
 template <typename T>
 hipError_t launch_t(const PrefillParams &p, hipStream_t stream) {
   const int bq = kRows / p.group;
-  const int n_qtiles = (p.max_query_len + bq - 1) / bq;
+  // At least one query tile per (sequence, kv head): its workgroup marks the
+  // rows of chunks longer than max_query_len (see the kernel's end).
+  const int n_qtiles = max(1, (p.max_query_len + bq - 1) / bq);
   const int64_t total = (int64_t)p.num_seqs * p.num_kv_heads * n_qtiles;
   if (total <= 0) return hipSuccess;
   if (total > (int64_t)1 << 30) return hipErrorInvalidValue;

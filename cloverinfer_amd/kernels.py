@@ -408,12 +408,15 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
 def chunked_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                     v_cache: torch.Tensor, block_tables: torch.Tensor,
                     context_lens: torch.Tensor, query_start_loc: torch.Tensor,
-                    max_query_len: int, scale: float | None = None) -> None:
+                    max_query_len: int | None, scale: float | None = None) -> None:
     """Causal attention of each sequence's new query rows over its paged context.
 
     Sequence s owns rows ``query_start_loc[s]:query_start_loc[s+1]`` of q/out;
     its new tokens are the last ones of its ``context_lens[s]`` cached tokens,
     and row i sees positions ``<= context_lens[s] - n_s + i``.
+    ``max_query_len`` must be at least every chunk length n_s (it sizes the
+    launch; rows past it come out as NaN); None computes it from
+    ``query_start_loc`` with one small device-to-host copy.
     """
     dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens, query_start_loc)
     _check_cache(k_cache, v_cache)
@@ -440,6 +443,8 @@ def chunked_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
         raise ValueError("block_tables must be a contiguous int32 [num_seqs, max_blocks] tensor")
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
+    if max_query_len is None:
+        max_query_len = int(query_start_loc.diff().max()) if num_seqs else 0
     a = _native.PrefillArgs()
     a.out, a.q = out.data_ptr(), q.data_ptr()
     a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()

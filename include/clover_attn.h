@@ -97,6 +97,9 @@ typedef struct clv_cache_args {
  * clv_reshape_and_cache first). Query row i of sequence s (0 <= i < n_s)
  * attends to cached positions p <= context_lens[s] - n_s + i (causal inside
  * the chunk, full view of everything cached before it).
+ * max_query_len sizes the launch and must be >= every n_s (the host cannot
+ * see query_start_loc, a device array): on the MFMA path, rows past it come
+ * out as NaN.
  */
 typedef struct clv_prefill_args {
   void *out;                      /* [num_tokens, num_heads, head_dim] */

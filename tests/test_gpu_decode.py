@@ -19,7 +19,7 @@ DEV = "cuda"
 
 def run_decode(q, k, v, tables, ctx, scale, partition_size=None, width=None, num_waves=0):
     qg = q.to(DEV)
-    out = torch.empty_like(qg)
+    out = torch.full_like(qg, float("nan"))  # a row the kernels leave unwritten shows as NaN
     bt = padded_tables(tables, width).to(DEV)
     cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
     kernels.paged_attention(out, qg, k.to(DEV), v.to(DEV), bt, cl, k.shape[1], max(ctx),
@@ -263,3 +263,26 @@ def test_config_long_context_splitk_fp16():
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"long-context P{partition}")
         assert_north_star_bar(got, ref, f"long32k fp16, 2 x 32768, partition {partition}")
+
+
+def test_decode_repeated_calls_shared_workspace():
+    """Ten calls of changing shapes, wave counts and dtypes on the same cached
+    workspace, with split-K calls in between on the same stream: every result
+    matches the oracle (nothing a call leaves in the workspace leaks into the
+    next one), empty contexts give zero rows."""
+    shapes = [([300, 1, 0, 4097, 77], 28, 4, 128, 0), ([5, 900, 17], 12, 12, 64, 37),
+              ([2050, 2050], 8, 2, 128, 1000), ([16, 33, 600, 1200, 3], 16, 1, 128, 7),
+              ([700] * 6, 32, 8, 128, 0)]
+    for rep in range(2):
+        for idx, (ctx, hq, hkv, d, w) in enumerate(shapes):
+            dtype = (torch.bfloat16, torch.float16, torch.float32)[(rep + idx) % 3]
+            print(f"repeated balanced rep {rep} shape {idx} {dtype} W={w}", flush=True)
+            q, k, v, tables, scale = case(500 + 10 * rep + idx, ctx, hq, hkv, d, 16, dtype)
+            got = run_decode(q, k, v, tables, ctx, scale, num_waves=w or 1024)
+            ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+            assert_attention_close(got, ref, what=f"rep {rep} shape {idx}")
+            for s, c in enumerate(ctx):
+                if c == 0:
+                    assert torch.equal(got[s].float(), torch.zeros(hq, d))
+            split = run_decode(q, k, v, tables, ctx, scale, partition_size=64)
+            assert_attention_close(split, ref, what=f"split-K between balanced calls {idx}")

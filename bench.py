@@ -373,10 +373,11 @@ def measure_decode(args, name):
         slots = torch.tensor([int(w["table_host"][s, (c - 1) // bs]) * bs + (c - 1) % bs
                               for s, c in enumerate(w["ctx"])], dtype=torch.int64, device=dev)
         append_bytes = 2 * kn.numel() * kn.element_size() * 2 + slots.numel() * 8
+        cache_list = [kernels.cache_args(kn, vn, kc, vc, slots) for kc, vc in pools]
 
         def append(i):
-            kc, vc = pools[i % copies]
-            kernels.reshape_and_cache(kn, vn, kc, vc, slots)
+            kernels._native.check(lib.clv_reshape_and_cache(cache_list[i % copies], stream),
+                                  "clv_reshape_and_cache")
 
         phases.append(append)
         names.append("reshape_and_cache")
@@ -475,8 +476,12 @@ def measure_prefill(args):
     out = torch.empty_like(q)
     scale = d ** -0.5
 
+    lib = kernels._native.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ca = kernels.cache_args(kn, vn, k, v, slots)
+
     def append(i):
-        kernels.reshape_and_cache(kn, vn, k, v, slots)
+        kernels._native.check(lib.clv_reshape_and_cache(ca, stream), "clv_reshape_and_cache")
 
     def attend(i):
         kernels.chunked_prefill(out, q, k, v, table, ctx_dev, qsl, new, scale=scale)

@@ -362,14 +362,7 @@ def splitk_reduce(a: _native.DecodeArgs, partition_size: int, workspace: torch.T
         stream), "clv_splitk_reduce")
 
 
-def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
-                      v_cache: torch.Tensor, slot_mapping: torch.Tensor,
-                      k_scale=None, v_scale=None) -> None:
-    """Write token i's ``key[i]``/``value[i]`` ([num_kv_heads, head_dim]) to cache slot
-    ``slot_mapping[i]`` (= block*block_size + offset; negative slots are skipped).
-    fp8 pools store e4m3(clamp(x / scale, -448, 448)) with per-kv-head
-    ``k_scale``/``v_scale``."""
-    dev = _require_device(key, value, k_cache, v_cache, slot_mapping)
+def _cache_args(key, value, k_cache, v_cache, slot_mapping) -> _native.CacheArgs:
     _check_cache(k_cache, v_cache)
     num_blocks, bs, num_kv_heads, head_dim = k_cache.shape
     if key.dim() != 3 or value.shape != key.shape or key.shape[1:] != (num_kv_heads, head_dim):
@@ -395,7 +388,32 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Ten
     a.num_tokens = key.shape[0]
     a.num_kv_heads, a.head_dim, a.block_size, a.num_blocks = num_kv_heads, head_dim, bs, num_blocks
     a.dtype = _dtype_code(key)
-    if fp8:
+    return a
+
+
+def cache_args(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+               v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> _native.CacheArgs:
+    """Validated C-ABI argument block of a KV append into fp32/fp16/bf16
+    pools (the tensors stay owned by the caller and must outlive every launch
+    made with it): a caller that appends into the same buffers every step
+    builds it once and calls ``clv_reshape_and_cache`` with it directly."""
+    _require_device(key, value, k_cache, v_cache, slot_mapping)
+    if k_cache.dtype == FP8:
+        raise ValueError("cache_args covers fp32/fp16/bf16 pools; fp8 pools take reshape_and_cache")
+    return _cache_args(key, value, k_cache, v_cache, slot_mapping)
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                      v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                      k_scale=None, v_scale=None) -> None:
+    """Write token i's ``key[i]``/``value[i]`` ([num_kv_heads, head_dim]) to cache slot
+    ``slot_mapping[i]`` (= block*block_size + offset; negative slots are skipped).
+    fp8 pools store e4m3(clamp(x / scale, -448, 448)) with per-kv-head
+    ``k_scale``/``v_scale``."""
+    dev = _require_device(key, value, k_cache, v_cache, slot_mapping)
+    a = _cache_args(key, value, k_cache, v_cache, slot_mapping)
+    if k_cache.dtype == FP8:
+        num_kv_heads = k_cache.shape[2]
         ks = kv_scales(k_scale, num_kv_heads, dev)
         vs = kv_scales(v_scale, num_kv_heads, dev)
         _native.check(_native.load().clv_reshape_and_cache_fp8(a, ks.data_ptr(), vs.data_ptr(),

@@ -80,3 +80,29 @@ def test_manager_writes_match_index_put():
     assert m2.block_tables["a"] == [3, 2]
     assert torch.equal(m2.k_cache[3, :, 0, 0].cpu(), torch.tensor([0.0, 1, 2, 3]))
     assert torch.equal(m2.v_cache[2, 0].cpu(), torch.full((2, 8), -4.0))
+
+
+def test_prebuilt_cache_args_reused_across_steps():
+    """An argument block built once with kernels.cache_args and launched
+    directly through the C ABI step after step writes what reshape_and_cache
+    writes (new values in the same source buffers each step)."""
+    g = torch.Generator().manual_seed(5)
+    nb, bs, hkv, d, n = 9, 16, 12, 64, 8
+    src_k = torch.empty(n, hkv, d, device=DEV)
+    src_v = torch.empty(n, hkv, d, device=DEV)
+    slots = torch.randperm(nb * bs, generator=g)[:n].to(DEV)
+    k_a = torch.zeros(nb, bs, hkv, d, device=DEV)
+    v_a = torch.zeros_like(k_a)
+    k_b, v_b = k_a.clone(), v_a.clone()
+    a = kernels.cache_args(src_k, src_v, k_a, v_a, slots)
+    lib = kernels._native.load()
+    for step in range(3):
+        src_k.copy_(torch.randn(n, hkv, d, generator=g))
+        src_v.copy_(torch.randn(n, hkv, d, generator=g))
+        kernels._native.check(lib.clv_reshape_and_cache(a, torch.cuda.current_stream().cuda_stream),
+                              "clv_reshape_and_cache")
+        kernels.reshape_and_cache(src_k, src_v, k_b, v_b, slots)
+        torch.cuda.synchronize()
+        assert torch.equal(k_a, k_b) and torch.equal(v_a, v_b), f"step {step}"
+    with pytest.raises(ValueError):
+        kernels.cache_args(src_k, src_v, k_a.to(torch.float16), v_a.to(torch.float16), slots)

@@ -182,6 +182,14 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base) {
                                            0x00020000);
 }
 
+// A buffer resource covering [base, base + num_bytes): a raw buffer load at a
+// lane offset at or past num_bytes returns zeros (the hardware range check)
+// and reads no memory; num_bytes = 0 makes every lane read zeros.
+__device__ __forceinline__ rsrc_t make_rsrc_range(const void *base, int num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, num_bytes,
+                                           0x00020000);
+}
+
 // Cache policy of a buffer load: kCacheDefault, or kCacheStream for data read
 // exactly once (the non-temporal hint: on MI355X streaming a large buffer this
 // way reads HBM at close to 90% of peak, against under 80% with the default).

@@ -65,10 +65,12 @@ constexpr float kRescaleLog2 = 8.f;     // lazy-rescale threshold (log2 units)
 // c0 + 4(i % 4) .. +3 of one row t_k, lane i gets column c0 + i of rows
 // t_0..t_3: four K-consecutive elements of an MFMA B operand. Two such reads
 // (rows of k-slots 0..3 and 4..7) make the lane's 8-element operand.
-__device__ __forceinline__ u32x4 vt_read(const uint16_t *lo, const uint16_t *hi) {
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)lo);
-  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)hi);
+// The reads take 32-bit LDS byte addresses: `lo` and `hi` are a common base
+// plus constants, which the instruction's offset field absorbs.
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ u32x4 vt_read(uint32_t lo, uint32_t hi) {
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(size_t)lo);
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(size_t)hi);
   const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
   return (u32x4){ua[0], ua[1], ub[0], ub[1]};
 }
@@ -195,7 +197,7 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   const int lrow = tid / CPR;
   const int wrow = WROWS * wave;  // first row of the wave's load instructions
   // Byte strides as 32-bit values (the launcher checks that a block's rows
-  // fit in 2^32 bytes).
+  // fit in 2^31 bytes, so 0x80000000 is past every block's range).
   const uint32_t sblk32 = (uint32_t)kv.sblk, stok32 = (uint32_t)kv.stok;
   const uint32_t bmask = (1u << kv.block_shift) - 1u;
   const uint32_t lane_off = (uint32_t)(lrow - wrow) * stok32 + (uint32_t)lchunk * 16u;
@@ -212,16 +214,22 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       rblk[i] = (tile < ntiles && t0 < kv_end) ? brow[t0 >> kv.block_shift] : -1;
     }
   };
+  // Rows are read through a buffer resource whose range is the rows of one
+  // block: a lane whose token is not readable (past the context, or in an
+  // unmapped block, which gets an empty range) reads zeros from the hardware
+  // range check, so there are no per-lane branches and no zero fills.
   auto load_tile = [&](int tile) {
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const uint32_t t0 = (uint32_t)(tile * kBK + wrow + RPP * i);
-      const bool ok = (unsigned)rblk[i] < kv.num_blocks && (int)t0 + (lrow - wrow) < kv_end;
-      const uint64_t wb = (uint64_t)(uint32_t)rblk[i] * sblk32 + (t0 & bmask) * stok32;
-      const u32x4 z = {0u, 0u, 0u, 0u};
+      const bool bok = (unsigned)rblk[i] < kv.num_blocks;
+      const bool ok = bok && (int)t0 + (lrow - wrow) < kv_end;
       rvalid[i] = ok;
-      kreg[i] = ok ? load_vec<u32x4>(kv.kbase + wb + lane_off) : z;
-      vreg[i] = ok ? load_vec<u32x4>(kv.vbase + wb + lane_off) : z;
+      const uint64_t boff = (uint64_t)(uint32_t)(bok ? rblk[i] : 0) * sblk32;
+      const int nrec = bok ? (int)(stok32 << kv.block_shift) : 0;
+      const uint32_t voff = ok ? (t0 & bmask) * stok32 + lane_off : 0x80000000u;
+      kreg[i] = buf_load<u32x4>(make_rsrc_range(kv.kbase + boff, nrec), voff);
+      vreg[i] = buf_load<u32x4>(make_rsrc_range(kv.vbase + boff, nrec), voff);
     }
   };
   // Stage the loaded rows into LDS buffer buf. The fast pass stores V as
@@ -323,7 +331,14 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     auto pv = [&](int g) {
       const uint16_t *vrow = &sV[(g >> 1) % 3][(32 * (g & 1) + 4 * j + (n16 >> 2)) * VROW +
                                                4 * (n16 & 3)];
-      auto vread = [&](int m) { return vt_read(vrow + 16 * m, vrow + 16 * VROW + 16 * m); };
+      // One base register per call, opaque to the compiler: left alone, it
+      // kept one hoisted address per read and rebuilt each of them from the
+      // ring slot with two VALU ops per read on every call.
+      uint32_t vbase = (uint32_t)(size_t)(const __attribute__((address_space(3))) uint16_t *)vrow;
+      asm volatile("" : "+v"(vbase));
+      auto vread = [&](int m) {
+        return vt_read(vbase + 32u * m, vbase + 32u * (VROW + m));  // rows +0 / +16
+      };
       // V operands go out PVD blocks ahead of their MFMAs (a rolling window,
       // kept in order by the scheduling barriers).
       constexpr int PVD = 3;
@@ -554,8 +569,8 @@ bool prefill_mfma_supported(DType dt, int head_dim, int block_size) {
 
 hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream) {
   // The tile loader computes addresses inside a block with 32-bit byte
-  // offsets; pools with larger blocks take the VALU kernel.
-  const uint64_t eb = 2, lim = (uint64_t)1 << 32;
+  // offsets below 2^31; pools with larger blocks take the VALU kernel.
+  const uint64_t eb = 2, lim = (uint64_t)1 << 31;
   const bool narrow = (uint64_t)p.kv_stride_block * eb < lim &&
                       ((uint64_t)p.kv_stride_token * eb << p.block_shift) < lim;
   if (p.group > kRows || !narrow) return launch_prefill_valu(p, dt, stream);

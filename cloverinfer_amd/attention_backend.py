@@ -24,6 +24,7 @@ reshape_and_cache launch plus one paged-decode launch, fed by:
 from __future__ import annotations
 
 import math
+import operator
 from typing import Dict, List, Optional
 
 import numpy as np
@@ -39,6 +40,11 @@ class _Request:
     def __init__(self, blocks: List[int], row: int):
         self.blocks = blocks  # blocks held, in table order
         self.row = row        # row of the device block table and of the host state
+
+
+_get_layer = operator.itemgetter("layer_idx")
+_get_rid = operator.itemgetter("request_id")
+_get_row = operator.attrgetter("row")
 
 
 def _align(n: int) -> int:
@@ -111,6 +117,14 @@ class GpuAttentionBackend:
         self._bshift = block_size.bit_length() - 1
         self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
         self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
+        # Device-side twins of the staging buffer and of the output, reused by
+        # every wave whose results go back to the host (such a call waits for
+        # them before it returns), and the fused launches built for them.
+        self._dstage: Optional[torch.Tensor] = None
+        self._dout: Optional[torch.Tensor] = None
+        self._launches: Dict[tuple, "kernels.AppendDecodeLaunch"] = {}
+        self._views: Dict[tuple, tuple] = {}  # device views into _dstage per batch shape
+        self._filled_host = False
         self.stats = {"decode_items": 0, "decode_launches": 0, "init_requests": 0}
 
     # ------------------------------------------------------------ pools
@@ -316,12 +330,12 @@ class GpuAttentionBackend:
         requests = self.requests
         if items:
             # The node's batch: one layer and scale, distinct known requests,
-            # checked with a few comprehensions instead of a loop per item.
-            layers = {it["layer_idx"] for it in items}
+            # checked with a few C-level passes instead of a loop per item.
+            layers = set(map(_get_layer, items))
             scales = {it.get("score_scale", 1.0) for it in items}
             if len(layers) == 1 and len(scales) == 1:
-                reqs = [requests.get(it["request_id"]) for it in items]
-                if None not in reqs and len({r.row for r in reqs}) == len(reqs):
+                reqs = list(map(requests.get, map(_get_rid, items)))
+                if None not in reqs and len(set(map(_get_row, reqs))) == len(reqs):
                     return self._run_wave(*self._payloads(items), reqs, int(layers.pop()),
                                           float(scales.pop()))
         out: List[torch.Tensor] = []
@@ -416,6 +430,7 @@ class GpuAttentionBackend:
             # converts dtypes), anything else takes the general path.
             try:
                 torch.stack(ts, out=host.view(n, *t0.shape))
+                self._filled_host = True  # every payload was a host tensor
                 return None
             except (RuntimeError, TypeError):
                 pass
@@ -456,25 +471,30 @@ class GpuAttentionBackend:
         kdt = self._append_dtype(ks[0].dtype)  # fp8 pools: quantised once, from the payload
 
         # One pinned buffer, one upload: q | k | v | int32 context lengths and
-        # rows | int64 slots and table updates (rows, columns, blocks). The
-        # table updates come last: their count is known only after the
-        # bookkeeping, and a wave takes at most one new block per request.
+        # rows | int64 slots | table updates (int64 flat table indices, then
+        # int32 blocks). The updates come last: their count is known only
+        # after the bookkeeping, and a wave takes at most one new block per
+        # request. Everything before them sits at offsets fixed by the batch
+        # shape, so their device views are built once per shape.
         qb = n * hq * d * torch.finfo(dt).bits // 8
         kb = n * hkv * d * torch.finfo(kdt).bits // 8
         o_k = _align(qb)
         o_v = o_k + _align(kb)
         o_i = o_v + _align(kb)
         o_w = o_i + _align(8 * n)
+        o_u = o_w + 8 * n
         nu_max = self.tables.pending_count() + n
-        buf = self._staging("wave", (o_w + 8 * (n + 3 * nu_max),), torch.uint8)
+        buf = self._staging("wave", (o_u + 12 * nu_max,), torch.uint8)
+        self._filled_host = False
         q = self._fill(qs, hq, d, dt, buf[:qb])
+        q_host = self._filled_host
         k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
         v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
 
         # Bookkeeping over the requests' rows: the new token of request i
         # goes to position pos[i] of this layer (a request whose blocks are
         # full takes one more first).
-        rows = np.fromiter((r.row for r in reqs), dtype=np.int64, count=n)
+        rows = np.fromiter(map(_get_row, reqs), dtype=np.int64, count=n)
         pos = self._lens[rows, layer]
         full = np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist()
         if len(full) > len(self.free_blocks):
@@ -488,44 +508,79 @@ class GpuAttentionBackend:
         nu = len(upd)
         applied = False
         try:
-            total = o_w + 8 * (n + 3 * nu)
+            total = o_u + 12 * nu
             narrow = buf[o_i:o_i + 8 * n].numpy().view(np.int32)
             narrow[:n] = lens
             narrow[n:] = rows
-            wide = buf[o_w:total].numpy().view(np.int64)
-            wide[:n] = slots
+            buf[o_w:o_u].numpy().view(np.int64)[:] = slots
             if nu:
-                wide[n:] = np.asarray(upd, dtype=np.int64).T.reshape(-1)
-            dev = buf[:total].to(self.device, non_blocking=True)
+                flat, blocks = self.tables.flat_updates(upd)
+                buf[o_u:o_u + 8 * nu].numpy().view(np.int64)[:] = flat
+                buf[o_u + 8 * nu:total].numpy().view(np.int32)[:] = blocks
+            if self._dstage is None or self._dstage.numel() < total:
+                self._dstage = torch.empty(max(2 * total, 1 << 20), dtype=torch.uint8,
+                                           device=self.device)
+                self._views.clear()
+            dev = self._dstage[:total]
+            dev.copy_(buf[:total], non_blocking=True)
             self._stage_done = torch.cuda.Event()
             self._stage_done.record()
-            if q is None:
-                q = dev[:qb].view(dt).view(n, hq, d)
-            if k is None:
-                k = dev[o_k:o_k + kb].view(kdt).view(n, hkv, d)
-            if v is None:
-                v = dev[o_v:o_v + kb].view(kdt).view(n, hkv, d)
-            wide_dev = dev[o_w:total].view(torch.int64)
+            vkey = (n, hq, hkv, d, dt, kdt)
+            views = self._views.get(vkey)
+            if views is None:
+                narrow_dev = self._dstage[o_i:o_i + 8 * n].view(torch.int32)
+                views = (self._dstage[:qb].view(dt).view(n, hq, d),
+                         self._dstage[o_k:o_k + kb].view(kdt).view(n, hkv, d),
+                         self._dstage[o_v:o_v + kb].view(kdt).view(n, hkv, d),
+                         narrow_dev[:n], narrow_dev[n:],
+                         self._dstage[o_w:o_u].view(torch.int64))
+                self._views[vkey] = views
+            q = views[0] if q is None else q
+            k = views[1] if k is None else k
+            v = views[2] if v is None else v
+            ctx_dev, rows_dev, slots_dev = views[3], views[4], views[5]
             if nu:
-                self.tables.apply(wide_dev[n:].view(3, nu), max(u[1] for u in upd))
+                self.tables.apply_flat(dev[o_u:o_u + 8 * nu].view(torch.int64),
+                                       dev[o_u + 8 * nu:total].view(torch.int32))
             applied = True
-            slots_dev = wide_dev[:n]
-            narrow_dev = dev[o_i:o_i + 8 * n].view(torch.int32)
-            ctx_dev = narrow_dev[:n]
-            bt = self.tables.rows(rows.tolist(), narrow_dev[n:])
-            ctx_out = torch.empty_like(q)
-            kp, vp = self.k_pools[layer], self.v_pools[layer]
-            max_len = int(lens.max())
-            if self.partition_size is None and kernels.append_fusable(q, kp, n):
-                # Append and decode in one call: the new rows land at position
-                # lens - 1, the slots computed above.
-                kernels.paged_attention_append(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len, k, v,
-                                               scale=score_scale)
+            if rows[-1] - rows[0] == n - 1 and (n < 3 or bool((np.diff(rows) == 1).all())):
+                bt = self.tables.rows_range(int(rows[0]), n)
             else:
-                self._append(k, v, layer, slots_dev)
-                kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
-                                        scale=score_scale, partition_size=self.partition_size,
-                                        k_scale=self.k_scales, v_scale=self.v_scales)
+                bt = self.tables.rows(rows.tolist(), rows_dev)
+            to_host = (not qs.is_cuda) if packed else (q_host or all(not t.is_cuda for t in qs))
+            if to_host:
+                # The call waits for its results: the output buffer is free
+                # again when it returns.
+                if self._dout is None or self._dout.numel() < q.numel() or \
+                        self._dout.dtype != dt:
+                    self._dout = torch.empty(q.numel(), dtype=dt, device=self.device)
+                ctx_out = self._dout[:q.numel()].view(q.shape)
+            else:
+                ctx_out = torch.empty_like(q)
+            max_len = int(lens.max())
+            # Append and decode in one call (the new rows land at position
+            # lens - 1, the slots computed above) where the fused kernel covers
+            # the shape; the launch is built once per batch shape, layer and
+            # scale (the pools are never reallocated).
+            lkey = (n, hq, layer, float(score_scale), dt, kdt, q.stride(), k.stride())
+            launch = self._launches.get(lkey) if self.partition_size is None else None
+            if launch is not None:
+                launch.update(ctx_out, q, bt, ctx_dev, max_len, k, v)
+                launch.launch()
+            else:
+                kp, vp = self.k_pools[layer], self.v_pools[layer]
+                if self.partition_size is None and kernels.append_fusable(q, kp, n):
+                    if len(self._launches) >= 256:
+                        self._launches.clear()
+                    launch = kernels.AppendDecodeLaunch(ctx_out, q, kp, vp, bt, ctx_dev, bs,
+                                                        max_len, k, v, scale=score_scale)
+                    self._launches[lkey] = launch
+                    launch.launch()
+                else:
+                    self._append(k, v, layer, slots_dev)
+                    kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
+                                            scale=score_scale, partition_size=self.partition_size,
+                                            k_scale=self.k_scales, v_scale=self.v_scales)
         except BaseException:
             self._lens[rows, layer] = pos
             if not applied:
@@ -538,13 +593,19 @@ class GpuAttentionBackend:
         # Outputs in each query's dtype and on its device: one copy for the
         # batch when the queries agree (the node's case), per item otherwise.
         qdt, qdev = q0.dtype, q0.device
-        if packed:
-            return ctx_out.to(device=qdev, dtype=qdt).view(n, 1, hq, d)
-        if all(t.dtype == qdt for t in qs) and (
-                (qdev.type == "cpu" and all(not t.is_cuda for t in qs))
-                or all(t.device == qdev for t in qs)):
-            res = ctx_out.to(device=qdev, dtype=qdt)
-            return list(res.view(n, 1, hq, d).unbind(0))
+        if packed or (all(t.dtype == qdt for t in qs) and (
+                (qdev.type == "cpu" and to_host) or all(t.device == qdev for t in qs))):
+            if qdev.type == "cpu":
+                # One copy into pinned host memory (a pageable destination goes
+                # through the driver's bounce buffer at a fraction of the rate),
+                # then wait for it.
+                res = torch.empty((n, 1, hq, d), dtype=qdt, pin_memory=True)
+                res.view(n, hq, d).copy_(ctx_out if dt == qdt else ctx_out.to(qdt),
+                                         non_blocking=True)
+                torch.cuda.current_stream(self.device).synchronize()
+            else:
+                res = ctx_out.to(device=qdev, dtype=qdt).view(n, 1, hq, d)
+            return res if packed else list(res.unbind(0))
         return [ctx_out[i:i + 1].to(device=t.device, dtype=t.dtype) for i, t in enumerate(qs)]
 
     def get_context_len(self, request_id: str) -> int:

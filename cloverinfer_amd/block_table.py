@@ -16,6 +16,7 @@ from __future__ import annotations
 
 from typing import List, Sequence, Tuple
 
+import numpy as np
 import torch
 
 
@@ -79,6 +80,18 @@ class DeviceBlockTable:
         upd, self._pending = self._pending, []
         return upd
 
+    def flat_updates(self, upd: List[Tuple[int, int, int]]):
+        """Host side of :meth:`apply_flat`: widens the table if a column is
+        past its width and returns the entries as (int64 flat indices into
+        the table, int32 blocks), numpy arrays to upload."""
+        a = np.asarray(upd, dtype=np.int64)
+        self._grow(self.table.shape[0], int(a[:, 1].max()) + 1)
+        return a[:, 0] * self.width + a[:, 1], a[:, 2].astype(np.int32)
+
+    def apply_flat(self, flat: torch.Tensor, blocks: torch.Tensor) -> None:
+        """One scatter of uploaded :meth:`flat_updates` into the table."""
+        self.table.view(-1).scatter_(0, flat, blocks)
+
     def apply(self, upd: torch.Tensor, max_column: int) -> None:
         """``upd``: int64 device tensor [3, P] of (row, column, block). One
         scatter into the flattened table (no host synchronisation)."""
@@ -90,6 +103,12 @@ class DeviceBlockTable:
         """Release a row (it is rewritten whole when reused)."""
         self._pending = [p for p in self._pending if p[0] != row]
         self._free_rows.append(row)
+
+    def rows_range(self, first: int, n: int) -> torch.Tensor:
+        """The table of the consecutive rows ``first .. first + n - 1`` (a
+        view). Flushes queued entries."""
+        self.flush()
+        return self.table[first:first + n]
 
     def rows(self, rows: Sequence[int], rows_dev: torch.Tensor | None = None) -> torch.Tensor:
         """The contiguous ``[len(rows), width]`` block table of these requests

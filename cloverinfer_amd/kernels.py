@@ -276,6 +276,60 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     )
 
 
+class AppendDecodeLaunch:
+    """A validated fused append + decode (clv_paged_decode_append) that can
+    be issued again: a caller whose batch keeps its shapes, pools and scale
+    from call to call (the AttentionNode's layer after layer) builds it once
+    and, per call, points it at that call's buffers with :meth:`update` (no
+    checks: the new tensors must have the shapes and strides of the ones it
+    was built with) before :meth:`launch`."""
+
+    def __init__(self, out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, block_tables: torch.Tensor, context_lens: torch.Tensor,
+                 block_size: int, max_context_len: int, key_new: torch.Tensor,
+                 value_new: torch.Tensor, scale: float | None = None, num_waves: int = 0):
+        self.device = _require_device(out, q, k_cache, v_cache, block_tables, context_lens,
+                                      key_new, value_new)
+        a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                         max_context_len, scale)
+        if not balanced_supported(a):
+            raise NotImplementedError("paged_attention_append covers the balanced decode's shapes only")
+        shape = (a.num_seqs, a.num_kv_heads, a.head_dim)
+        if key_new.shape != shape or value_new.shape != shape:
+            raise ValueError(f"key_new/value_new must be {shape}, got {tuple(key_new.shape)} and "
+                             f"{tuple(value_new.shape)}")
+        if key_new.dtype != k_cache.dtype or value_new.dtype != k_cache.dtype:
+            raise ValueError("key_new/value_new dtype must match the cache dtype")
+        if key_new.stride() != value_new.stride() or key_new.stride(2) != 1:
+            key_new, value_new = key_new.contiguous(), value_new.contiguous()
+        self.args = a
+        self.num_waves = num_waves
+        self.key_ptr, self.value_ptr = key_new.data_ptr(), value_new.data_ptr()
+        self.kv_new_strides = (key_new.stride(0), key_new.stride(1))
+        lib = _native.load()
+        self.workspace_bytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads,
+                                                                a.num_kv_heads, a.head_dim,
+                                                                num_waves)
+        self._fn = lib.clv_paged_decode_append
+
+    def update(self, out: torch.Tensor, q: torch.Tensor, block_tables: torch.Tensor,
+               context_lens: torch.Tensor, max_context_len: int, key_new: torch.Tensor,
+               value_new: torch.Tensor) -> None:
+        a = self.args
+        a.out, a.q = out.data_ptr(), q.data_ptr()
+        a.block_tables, a.max_blocks_per_seq = block_tables.data_ptr(), block_tables.shape[1]
+        a.context_lens = context_lens.data_ptr()
+        a.max_context_len = int(max_context_len)
+        self.key_ptr, self.value_ptr = key_new.data_ptr(), value_new.data_ptr()
+
+    def launch(self) -> None:
+        """Issue on the current stream (with that stream's workspace)."""
+        ws = splitk_workspace(self.device, self.workspace_bytes)
+        _native.check(self._fn(self.args, self.key_ptr, self.value_ptr, *self.kv_new_strides,
+                               self.num_waves, ws.data_ptr(), ws.numel(), _stream(self.device)),
+                      "clv_paged_decode_append")
+
+
 def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                            v_cache: torch.Tensor, block_tables: torch.Tensor,
                            context_lens: torch.Tensor, block_size: int, max_context_len: int,
@@ -289,27 +343,8 @@ def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Te
     :func:`reshape_and_cache` with those slots followed by
     :func:`paged_attention`; covers the shapes of the balanced decode
     (:func:`append_fusable`), raises otherwise."""
-    dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens, key_new, value_new)
-    a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
-                     max_context_len, scale)
-    if not balanced_supported(a):
-        raise NotImplementedError("paged_attention_append covers the balanced decode's shapes only")
-    shape = (a.num_seqs, a.num_kv_heads, a.head_dim)
-    if key_new.shape != shape or value_new.shape != shape:
-        raise ValueError(f"key_new/value_new must be {shape}, got {tuple(key_new.shape)} and "
-                         f"{tuple(value_new.shape)}")
-    if key_new.dtype != k_cache.dtype or value_new.dtype != k_cache.dtype:
-        raise ValueError("key_new/value_new dtype must match the cache dtype")
-    if key_new.stride() != value_new.stride() or key_new.stride(2) != 1:
-        key_new, value_new = key_new.contiguous(), value_new.contiguous()
-    lib = _native.load()
-    nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
-                                              a.head_dim, num_waves)
-    ws = splitk_workspace(dev, nbytes)
-    _native.check(lib.clv_paged_decode_append(a, key_new.data_ptr(), value_new.data_ptr(),
-                                              key_new.stride(0), key_new.stride(1), num_waves,
-                                              ws.data_ptr(), ws.numel(), _stream(dev)),
-                  "clv_paged_decode_append")
+    AppendDecodeLaunch(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                       max_context_len, key_new, value_new, scale, num_waves).launch()
 
 
 def append_fusable(q: torch.Tensor, k_cache: torch.Tensor, num_seqs: int) -> bool:

@@ -363,6 +363,7 @@ def measure_decode(args, name):
 
     phases, names = [], []
     append_bytes = 0
+    fused = None
     if cfg.get("append"):
         # The step's append: token ctx - 1 of every sequence (its new row)
         # through reshape_and_cache into the pool copy the step decodes.
@@ -379,8 +380,17 @@ def measure_decode(args, name):
             kernels._native.check(lib.clv_reshape_and_cache(cache_list[i % copies], stream),
                                   "clv_reshape_and_cache")
 
-        phases.append(append)
-        names.append("reshape_and_cache")
+        if mode == "single" and kernels.append_fusable(w["q"], w["k"], len(w["ctx"])):
+            # The step as the backend runs it: one single-pass launch that
+            # writes token ctx - 1 of every sequence and attends over it
+            # (clv_paged_decode_append); the two-launch form (append kernel,
+            # then decode) is timed beside it.
+            fused = [kernels.AppendDecodeLaunch(out, w["q"], kc, vc, w["table"], w["ctx_dev"],
+                                                w["bs"], max_ctx, kn, vn, scale=w["scale"])
+                     for kc, vc in pools]
+        else:
+            phases.append(append)
+            names.append("reshape_and_cache")
 
     def first_half(i):
         a = args_list[i % copies]
@@ -398,19 +408,36 @@ def measure_decode(args, name):
         else:
             kernels.splitk_reduce(a, part, ws, stream)
 
-    phases.append(first_half)
-    names.append("paged_decode")
-    if mode != "single":
-        phases.append(second_half)
-        names.append("merge")
+    two_launch = None
+    if fused is not None:
+        log(f"{name}: two-launch form (reshape_and_cache, then the decode), {args.steps} steps")
+        ms2, ev2 = time_steps(args, [append, first_half])
+        two_launch = {"ms_per_step": ms2, "kernels_us": {"reshape_and_cache": ev2[0][0],
+                                                         "paged_decode": ev2[1][0]}}
+        calls = [f.bind() for f in fused]
+
+        def fused_step(i):
+            kernels._native.check(calls[i % copies](), "clv_paged_decode_append")
+
+        phases.append(fused_step)
+        names.append("paged_decode_append")
+    else:
+        phases.append(first_half)
+        names.append("paged_decode")
+        if mode != "single":
+            phases.append(second_half)
+            names.append("merge")
     log(f"{name}: warmup {args.warmup}, {args.steps} steps (schedule {mode}, partition "
         f"{part if mode == 'split' else 0}, {copies} pool copies)")
     ms, ev = time_steps(args, phases)
-    dec_us = ev[names.index("paged_decode")][0]
+    dec_us = ev[names.index("paged_decode_append" if fused is not None else "paged_decode")][0]
     log(f"{name}: step {ms:.4f} ms, " + ", ".join(f"{n} {e[0]:.1f} us" for n, e in zip(names, ev)))
     step_bytes = w["algo_bytes"] + append_bytes
     kernel = {"balanced": "paged_decode_stream", "split": "paged_decode_mfma (split-K partials)",
               "single": "paged_decode_mfma (single pass)"}[mode]
+    kernel_bytes = w["algo_bytes"]
+    if fused is not None:
+        kernel, kernel_bytes = "paged_decode_mfma (single pass, fused append)", step_bytes
     traffic, note = traffic_for(name)
     entry = {
         "workload": cfg["workload"],
@@ -427,8 +454,10 @@ def measure_decode(args, name):
         "decode_algorithmic_bytes": w["algo_bytes"],
         "kernels_us": {n: e[0] for n, e in zip(names, ev)},
         "kernels_us_median": {n: e[1] for n, e in zip(names, ev)},
-        "roofline": roofline("hbm", kernel, w["algo_bytes"] / (dec_us * 1e-6) / 1e9, traffic, note),
+        "roofline": roofline("hbm", kernel, kernel_bytes / (dec_us * 1e-6) / 1e9, traffic, note),
     }
+    if two_launch is not None:
+        entry["two_launch"] = two_launch
     # Host copies for the CPU baseline: each sequence's context gathered into
     # the reference backend's contiguous [L, Hkv, D] form (untimed setup).
     from oracle import attention as oa

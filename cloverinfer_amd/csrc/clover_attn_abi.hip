@@ -145,6 +145,10 @@ int fill_decode(const clv_decode_args *a, clv::DecodeParams *p) {
   return CLV_OK;
 }
 
+// Longest context for which clv_paged_decode_append runs the single pass
+// (the schedule the Python layer picks for such batches: no merge launch).
+constexpr int32_t kAppendSinglePassMaxLen = 512;
+
 int launch_decode(const clv::DecodeParams &p, int dtype, int block_size, hipStream_t stream) {
   const DType dt = (DType)dtype;
   hipError_t err;
@@ -473,6 +477,27 @@ int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const
                             int64_t new_stride_seq, int64_t new_stride_head, int32_t num_waves,
                             void *workspace, size_t workspace_bytes, clv_stream_t stream) {
   clv::DecodeParams p;
+  // Short contexts (the single-pass schedule's range) with at most 16 query
+  // heads per kv head: one grid launch that appends and attends, no merge.
+  if (a != nullptr && num_waves <= 0 && a->max_context_len <= kAppendSinglePassMaxLen &&
+      a->num_kv_heads > 0 && a->num_heads % a->num_kv_heads == 0 &&
+      a->num_heads / a->num_kv_heads <= 16 &&
+      clv::decode_mfma_supported((DType)a->dtype, a->head_dim, a->block_size)) {
+    const int st = fill_decode(a, &p);
+    if (st != CLV_OK || p.num_seqs == 0) return st;
+    const int eb = elem_bytes(a->dtype);
+    if (!key_new || !value_new || !aligned16(key_new) || !aligned16(value_new) ||
+        !stride16(new_stride_seq, eb) || !stride16(new_stride_head, eb))
+      return CLV_EINVAL;
+    p.partition_size = 0;
+    p.key_new = key_new;
+    p.value_new = value_new;
+    p.new_stride_seq = new_stride_seq;
+    p.new_stride_head = new_stride_head;
+    return clv::launch_decode_mfma_append(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+               ? CLV_OK
+               : CLV_ELAUNCH;
+  }
   const int st = fill_balanced(a, num_waves, workspace, workspace_bytes, &p);
   if (st != CLV_OK || p.num_seqs == 0) return st;
   const int eb = elem_bytes(a->dtype);

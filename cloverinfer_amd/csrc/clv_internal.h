@@ -93,6 +93,9 @@ enum class DType : int { F32 = 0, F16 = 1, BF16 = 2 };
 // Launchers return hipSuccess or the launch error. Shapes are pre-validated.
 hipError_t launch_reshape_and_cache(const CacheParams &p, hipStream_t stream);
 hipError_t launch_decode_mfma(const DecodeParams &p, DType dt, hipStream_t stream);
+// Single-pass grid decode that first writes key_new/value_new[s] at position
+// context_lens[s] - 1 (partition_size 0, one query-head chunk per kv head).
+hipError_t launch_decode_mfma_append(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_decode_valu(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_splitk_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream);

@@ -64,7 +64,14 @@ __device__ __forceinline__ OutDesc<T> out_desc(const DecodeParams &p, int s, int
 // with the loads of its next step in flight while the current one is
 // computed (two register sets), and the waves' partials are merged in LDS.
 // Ring depths: a third register set measured 3-4 % slower.
-template <typename T, int D, int NW, bool UNI>
+//
+// APPEND (single pass, one query-head chunk per kv head): the workgroup first
+// writes sequence s's new key/value row of its kv head at position
+// context_lens[s] - 1 (when that position is attended), then attends over it.
+// The barrier's workgroup-scope release/acquire orders those stores before
+// every wave's loads (the waves of a workgroup share one CU's caches), and no
+// other workgroup reads the row.
+template <typename T, int D, int NW, bool UNI, bool APPEND = false>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
   typedef typename GridWave<T, D, UNI>::type W;
@@ -78,6 +85,28 @@ paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
   const int h0 = kvh * p.group + g0;
 
   const int ctx = clamp_ctx(p, s);
+  if constexpr (APPEND) {
+    if (ctx > 0 && ctx == p.context_lens[s]) {
+      const int pos = ctx - 1;
+      const int blk = tables[(int64_t)s * p.max_blocks_per_seq + (pos >> p.block_shift)];
+      if ((unsigned)blk < (unsigned)p.num_blocks) {
+        const int64_t row = (int64_t)blk * p.kv_stride_block +
+                            (int64_t)(pos & ((1 << p.block_shift) - 1)) * p.kv_stride_token +
+                            (int64_t)kvh * p.kv_stride_head;
+        const int64_t src = (int64_t)s * p.new_stride_seq + (int64_t)kvh * p.new_stride_head;
+        constexpr int C16 = D * (int)sizeof(T) / 16;  // 16-byte chunks per row
+        constexpr int E16 = 16 / (int)sizeof(T);
+        for (int i = threadIdx.x; i < 2 * C16; i += NW * 64) {
+          const bool val = i >= C16;
+          const int c = val ? i - C16 : i;
+          const T *from = (const T *)(val ? p.value_new : p.key_new) + src + c * E16;
+          T *to = (T *)(val ? p.v_cache : p.k_cache) + row + c * E16;
+          store_vec<u32x4>(to, load_vec<u32x4>(from));
+        }
+      }
+    }
+    __syncthreads();
+  }
   int t_begin = 0, t_end = ctx;
   if (p.partition_size > 0) {
     t_begin = blockIdx.x * p.partition_size;
@@ -197,17 +226,24 @@ __global__ void __launch_bounds__(256) splitk_reduce(const DecodeParams p) {
   lse_merge<T, D, 4>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 1, D, nparts, dst, smem);
 }
 
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, bool APPEND = false>
 hipError_t launch_mfma_tdw(const DecodeParams &p, hipStream_t stream) {
   const dim3 grid(p.partition_size > 0 ? (unsigned)p.max_parts : 1u,
                   (unsigned)(p.num_kv_heads * p.n_gchunks), (unsigned)p.num_seqs);
   if (p.block_shift >= 4)
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true>), grid, dim3(NW * 64), 0, stream, p,
-                       p.block_tables);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true, APPEND>), grid, dim3(NW * 64), 0,
+                       stream, p, p.block_tables);
   else
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false>), grid, dim3(NW * 64), 0, stream, p,
-                       p.block_tables);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false, APPEND>), grid, dim3(NW * 64), 0,
+                       stream, p, p.block_tables);
   return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_mfma_append_t(const DecodeParams &p, hipStream_t stream) {
+  if (p.head_dim == 128) return launch_mfma_tdw<T, 128, 4, true>(p, stream);
+  if (p.head_dim == 64) return launch_mfma_tdw<T, 64, 4, true>(p, stream);
+  return hipErrorInvalidValue;
 }
 
 // Waves per workgroup: a single pass splits each (possibly long) context over
@@ -290,6 +326,14 @@ hipError_t launch_decode_mfma(const DecodeParams &p, DType dt, hipStream_t strea
   if (dt == DType::BF16) return launch_mfma_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_mfma_t<_Float16>(p, stream);
   if (dt == DType::F32) return launch_mfma_t<float>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_decode_mfma_append(const DecodeParams &p, DType dt, hipStream_t stream) {
+  if (p.partition_size != 0 || p.n_gchunks != 1) return hipErrorInvalidValue;
+  if (dt == DType::BF16) return launch_mfma_append_t<__bf16>(p, stream);
+  if (dt == DType::F16) return launch_mfma_append_t<_Float16>(p, stream);
+  if (dt == DType::F32) return launch_mfma_append_t<float>(p, stream);
   return hipErrorInvalidValue;
 }
 

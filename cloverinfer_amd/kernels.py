@@ -8,6 +8,7 @@ call goes through ``libclover_attn.so``; tensors must live on a HIP device.
 """
 from __future__ import annotations
 
+import functools
 import math
 import threading
 
@@ -329,6 +330,16 @@ class AppendDecodeLaunch:
                                self.num_waves, ws.data_ptr(), ws.numel(), _stream(self.device)),
                       "clv_paged_decode_append")
 
+    def bind(self):
+        """A callable that reissues this launch, as it stands now, on the
+        current stream with no further Python work beyond the C call (for a
+        caller that replays one step over fixed buffers); it returns the C
+        status code."""
+        ws = splitk_workspace(self.device, self.workspace_bytes)
+        return functools.partial(self._fn, self.args, self.key_ptr, self.value_ptr,
+                                 *self.kv_new_strides, self.num_waves, ws.data_ptr(), ws.numel(),
+                                 _stream(self.device))
+
 
 def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                            v_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -341,7 +352,10 @@ def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Te
     ``context_lens[s] - 1`` (slot from its block-table row), then ``out`` =
     :func:`paged_attention` over all ``context_lens[s]`` tokens. Equal to
     :func:`reshape_and_cache` with those slots followed by
-    :func:`paged_attention`; covers the shapes of the balanced decode
+    :func:`paged_attention` with the schedule :func:`choose_schedule` picks:
+    batches whose contexts fit the single pass (at most 512 tokens, at most 16
+    query heads per kv head, ``num_waves`` 0) are one single-pass launch,
+    longer ones the balanced decode. Covers the shapes of the balanced decode
     (:func:`append_fusable`), raises otherwise."""
     AppendDecodeLaunch(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
                        max_context_len, key_new, value_new, scale, num_waves).launch()

@@ -239,7 +239,11 @@ int clv_paged_decode_balanced_noalloc(const clv_decode_args *args, int32_t num_w
  * clv_paged_decode_balanced, and the same shapes and workspace as the latter
  * (CLV_EUNSUPPORTED otherwise). For 16-bit pools with head_dim 128,
  * block_size >= 16 and at most 16 query heads per kv head, the decode kernel
- * writes the rows itself (no separate append launch). A sequence appends nothing when
+ * writes the rows itself (no separate append launch). With num_waves <= 0,
+ * max_context_len <= 512 and at most 16 query heads per kv head (fp32, fp16
+ * or bf16 pools, head_dim 64 or 128, block_size >= 4), the call is instead
+ * one single-pass launch that appends and attends (as clv_paged_decode: no
+ * merge; the workspace is not used). A sequence appends nothing when
  * context_lens[s] is outside [1, min(max_context_len,
  * max_blocks_per_seq*block_size)] or the slot's block-table entry is outside
  * [0, num_blocks). k_cache and v_cache are written. No counterpart kernel

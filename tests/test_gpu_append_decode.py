@@ -1,9 +1,11 @@
 """Fused append + decode (clv_paged_decode_append) against the two-call form
-(reshape_and_cache with the same slots, then the balanced decode) and the
-fp32 oracle: pools bit for bit, outputs equal to the two-call result and
-within the parity bar of the oracle. Three consecutive steps per case, so
-contexts cross block borders; every slot not yet written holds NaN, so a
-read of a stale new-token slot shows up in the output."""
+(reshape_and_cache with the same slots, then the decode schedule the fused
+call runs: the single pass for contexts of at most 512 tokens and at most 16
+query heads per kv head, the balanced decode otherwise) and the fp32 oracle:
+pools bit for bit, outputs equal to the two-call result and within the
+parity bar of the oracle. Three consecutive steps per case, so contexts
+cross block borders; every slot not yet written holds NaN, so a read of a
+stale new-token slot shows up in the output."""
 import math
 
 import pytest
@@ -21,6 +23,13 @@ def _same_bits(a, b):
     return torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+def _fused_schedule(hq, hkv, max_len):
+    """paged_attention keyword arguments of the schedule the fused call runs."""
+    if max_len <= 512 and hq // hkv <= 16:
+        return {"partition_size": 0}
+    return {"num_waves": kernels._native.load().clv_default_num_waves()}
+
+
 @pytest.mark.parametrize("hq,hkv,d,bs,dtype", [
     (28, 4, 128, 16, torch.bfloat16),   # written inside the decode kernel
     (32, 8, 128, 32, torch.float16),    # idem, larger blocks
@@ -31,10 +40,13 @@ def _same_bits(a, b):
     (28, 4, 128, 16, torch.float32),    # fp32 pools: append kernel (4-byte rows), fp32 MFMA wave
     (16, 2, 64, 8, torch.float32),      # idem, head_dim 64, block_size 8
 ])
-def test_fused_append_decode(hq, hkv, d, bs, dtype):
-    ctx0 = [1, 15, 16, 31, 100, 0, 47]  # 0: no new token, zero output, pool untouched
+@pytest.mark.parametrize("long", [False, True], ids=["single-pass", "balanced"])
+def test_fused_append_decode(hq, hkv, d, bs, dtype, long):
+    # 0: no new token, zero output, pool untouched; 600: past the single
+    # pass's range, so the call takes the balanced decode
+    ctx0 = [1, 15, 16, 31, 600 if long else 100, 0, 47]
     steps = 3
-    print(f"append+decode hq={hq} hkv={hkv} d={d} bs={bs} {dtype}", flush=True)
+    print(f"append+decode hq={hq} hkv={hkv} d={d} bs={bs} {dtype} long={long}", flush=True)
     cap = [c + steps for c in ctx0]
     k, v, tables = make_paged_kv(hq + d + bs, cap, hkv, d, bs, dtype, spare_blocks=2)
     # positions >= the starting context hold stale NaN until appended
@@ -62,9 +74,8 @@ def test_fused_append_decode(hq, hkv, d, bs, dtype):
                  for t, c in zip(tables, grow)]
         kernels.reshape_and_cache(kn, vn, ku, vu, torch.tensor(slots, dtype=torch.int64, device=DEV))
         out_u = torch.empty_like(q)
-        # the balanced schedule with the fused call's (default) wave count
         kernels.paged_attention(out_u, q, ku, vu, bt, lens, bs, max(grow), scale=scale,
-                                num_waves=kernels._native.load().clv_default_num_waves())
+                                **_fused_schedule(hq, hkv, max(grow)))
         torch.cuda.synchronize()
         assert _same_bits(kf, ku) and _same_bits(vf, vu), f"pools differ at step {step}"
         assert torch.equal(out_f, out_u), f"fused output differs from the two-call form, step {step}"
@@ -74,9 +85,11 @@ def test_fused_append_decode(hq, hkv, d, bs, dtype):
         ctx = grow
 
 
-def test_fused_append_out_of_range_positions():
+@pytest.mark.parametrize("num_waves", [0, 1024], ids=["single-pass", "balanced"])
+def test_fused_append_out_of_range_positions(num_waves):
     """Contexts past max_context_len and block-table entries outside the pool
-    append nothing (as the slot form with a skipped slot would)."""
+    append nothing (as the slot form with a skipped slot would), in the
+    single-pass and the balanced form of the call."""
     hq, hkv, d, bs, dtype = 8, 2, 128, 16, torch.bfloat16
     k, v, tables = make_paged_kv(3, [40, 40], hkv, d, bs, dtype, spare_blocks=1)
     tables[1][2] = 10_000  # position 32.. of sequence 1 maps outside the pool
@@ -87,8 +100,10 @@ def test_fused_append_out_of_range_positions():
     vn = torch.randn(2, hkv, d).to(dtype).to(DEV)
     lens = torch.tensor([40, 40], dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
-    kernels.paged_attention_append(out, q, kf, vf, bt, lens, bs, 39, kn, vn)  # 40 > max_context_len
+    kernels.paged_attention_append(out, q, kf, vf, bt, lens, bs, 39, kn, vn,  # 40 > max_context_len
+                                   num_waves=num_waves)
     kernels.paged_attention_append(out, q, kf, vf, bt, torch.tensor([0, 35], dtype=torch.int32,
-                                                                     device=DEV), bs, 40, kn, vn)
+                                                                     device=DEV), bs, 40, kn, vn,
+                                   num_waves=num_waves)
     torch.cuda.synchronize()
     assert _same_bits(kf.cpu(), k) and _same_bits(vf.cpu(), v)

@@ -162,9 +162,9 @@ def _event_us(ev, a: int, b: int):
 
 
 def time_steps(args, phases):
-    """Run W untimed steps, then K steps timed by wall clock (synchronised on
-    both sides), then K more steps with HIP events between the phases of each
-    step. ``phases``: callables run in order as one step; each takes the step
+    """After args.settle seconds of untimed steps (see below), run W untimed
+    steps, then K steps timed by wall clock (synchronised on both sides), then
+    K more steps with HIP events between the phases of each step. ``phases``: callables run in order as one step; each takes the step
     index. Returns (ms per step, [(mean us, median us) per phase])."""
     import torch
 
@@ -172,6 +172,15 @@ def time_steps(args, phases):
         for ph in phases:
             ph(i)
 
+    # GPU clock settle, untimed and before the warm-up: MI355X raises its
+    # engine clock over the first tens of milliseconds of sustained work (the
+    # prefill kernel took 496 us on its 5th call and 399 us on its 45th, same
+    # inputs), and the workload set-up before each measurement leaves the GPU
+    # idle. Steps run one at a time, synchronised, for args.settle seconds.
+    t_end = time.perf_counter() + getattr(args, "settle", 0.0)
+    while time.perf_counter() < t_end:
+        step(0)
+        torch.cuda.synchronize()
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -182,11 +191,13 @@ def time_steps(args, phases):
     ms = (time.perf_counter() - t0) / args.steps * 1e3
     # HIP events on the stream the kernels run on. A leading device-side
     # sleep keeps the GPU busy while every launch is queued, so host launch
-    # gaps stay out of the event intervals.
+    # gaps stay out of the event intervals; it is sized to the queueing time
+    # (about 100K cycles, some 50 us, per step), since a long spin lets the
+    # engine clock drop before the timed kernels run.
     stream = torch.cuda.current_stream()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)]
           for _ in range(args.steps)]
-    torch.cuda._sleep(50_000_000)
+    torch.cuda._sleep(min(50_000_000, 100_000 * max(1, args.steps)))
     for i, e in enumerate(ev):
         e[0].record(stream)
         for j, ph in enumerate(phases):
@@ -601,6 +612,7 @@ def result_line(args, entries, head: str):
         res["cpu_baseline"] = e["cpu_baseline"]
     if len(entries) > 1:
         res["configs"] = entries
+    res["gpu_clock_settle_s"] = args.settle
     res["sources_sha256"] = sources_sha256()[:16]
     return res
 
@@ -756,6 +768,9 @@ def main() -> int:
     ap.add_argument("--waves", type=int, default=0,
                     help="waves of the balanced decode (0 = device default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--settle", type=float, default=0.2,
+                    help="seconds of untimed, synchronised steps before each workload's "
+                         "warm-up, so that the GPU clock has ramped up (0: none)")
     ap.add_argument("--cpu-budget", type=float, default=0.0,
                     help="seconds of CPU baseline work per workload (0: the built-in "
                          "per-workload budgets, 5-10 s)")

@@ -621,7 +621,8 @@ def bench_decode_fp8(args):
     """The GQA Qwen2.5-7B decode batch with fp8 (OCP e4m3) pools: K/V are
     the same seeded N(0,1) data stored as e4m3 with scale 1 per kv head; q
     and out stay bf16. A step is one clv_paged_decode_fp8 call (stream decode
-    + merge)."""
+    + merge), issued as its two halves (clv_paged_decode_fp8_partials, then
+    clv_balanced_reduce) so that the roofline times the decode kernel alone."""
     import torch
     from cloverinfer_amd import kernels
 
@@ -643,19 +644,26 @@ def bench_decode_fp8(args):
     waves = args.waves or lib.clv_default_num_waves_fp8()
     ws = kernels.splitk_workspace(dev, kernels.balanced_workspace_bytes(a, waves))
 
-    def step(i):
-        kernels._native.check(lib.clv_paged_decode_fp8(a, ones.data_ptr(), ones.data_ptr(),
-                                                       waves, ws.data_ptr(), ws.numel(),
-                                                       stream.cuda_stream), "clv_paged_decode_fp8")
+    # clv_paged_decode_fp8 is the fp8 stream kernel then the merge; issued as
+    # its two halves so that each is timed on its own.
+    def partials(i):
+        kernels._native.check(lib.clv_paged_decode_fp8_partials(
+            a, ones.data_ptr(), ones.data_ptr(), waves, ws.data_ptr(), ws.numel(),
+            stream.cuda_stream), "clv_paged_decode_fp8_partials")
 
-    ms, ev = time_steps(args, [step])
+    def merge(i):
+        kernels._native.check(lib.clv_balanced_reduce(a, waves, ws.data_ptr(), ws.numel(),
+                                                      stream.cuda_stream), "clv_balanced_reduce")
+
+    ms, ev = time_steps(args, [partials, merge])
     call_us, call_med = ev[0]
     ctx = w["ctx"]
     kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * 1 * 2
     qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * 2 * 2
     tbl_bytes = sum(math.ceil(c / w["bs"]) for c in ctx) * 4 + len(ctx) * 4
     algo = kv_bytes + qo_bytes + tbl_bytes
-    log(f"step {ms:.4f} ms, decode + merge {call_us:.1f} us")
+    merge_us, merge_med = ev[1]
+    log(f"step {ms:.4f} ms, decode {call_us:.1f} us, merge {merge_us:.1f} us")
     traffic, note = traffic_for("qwen7b_fp8")
     return {
         "metric": "decode-attn HBM GB/s, fp8 KV pools, GQA-7B shape, 1 GPU",
@@ -669,10 +677,10 @@ def bench_decode_fp8(args):
                    "total_context_tokens": sum(ctx), "algorithmic_bytes_per_step": algo,
                    "seed": cfg["seed"]},
         "tokens_per_s": len(ctx) / (ms * 1e-3),
-        "kernels_us": {"paged_decode_fp8_with_merge": call_us},
-        "kernels_us_median": {"paged_decode_fp8_with_merge": call_med},
-        "roofline": roofline("hbm", "paged_decode_stream (fp8) + merge",
-                             algo / (call_us * 1e-6) / 1e9, traffic, note),
+        "kernels_us": {"paged_decode": call_us, "merge": merge_us},
+        "kernels_us_median": {"paged_decode": call_med, "merge": merge_med},
+        "roofline": roofline("hbm", "paged_decode_stream (fp8)", algo / (call_us * 1e-6) / 1e9,
+                             traffic, note),
     }
 
 

@@ -162,6 +162,10 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
     ),
+    "clv_paged_decode_fp8_partials": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
     "clv_balanced_workspace_bytes": (ctypes.c_size_t, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "clv_default_num_waves": (_c_i32, []),
     "clv_default_num_waves_fp8": (_c_i32, []),

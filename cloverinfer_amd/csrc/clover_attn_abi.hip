@@ -521,6 +521,16 @@ int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const
 int clv_paged_decode_fp8(const clv_decode_args *a, const float *k_scales, const float *v_scales,
                          int32_t num_waves, void *workspace, size_t workspace_bytes,
                          clv_stream_t stream) {
+  if (num_waves <= 0) num_waves = clv_default_num_waves_fp8();
+  const int rc = clv_paged_decode_fp8_partials(a, k_scales, v_scales, num_waves, workspace,
+                                               workspace_bytes, stream);
+  if (rc != CLV_OK) return rc;
+  return clv_balanced_reduce(a, num_waves, workspace, workspace_bytes, stream);
+}
+
+int clv_paged_decode_fp8_partials(const clv_decode_args *a, const float *k_scales,
+                                  const float *v_scales, int32_t num_waves, void *workspace,
+                                  size_t workspace_bytes, clv_stream_t stream) {
   if (a == nullptr) return CLV_EINVAL;
   if (a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
   if (a->head_dim != 128 || a->block_size < 16) return CLV_EUNSUPPORTED;
@@ -540,9 +550,9 @@ int clv_paged_decode_fp8(const clv_decode_args *a, const float *k_scales, const 
   p.kv_fp8 = 1;
   p.k_scales = k_scales;
   p.v_scales = v_scales;
-  const hipStream_t s = (hipStream_t)stream;
-  if (clv::launch_decode_stream(p, (DType)a->dtype, s) != hipSuccess) return CLV_ELAUNCH;
-  return clv::launch_stream_reduce(p, (DType)a->dtype, s) == hipSuccess ? CLV_OK : CLV_ELAUNCH;
+  return clv::launch_decode_stream(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
 }
 
 int clv_chunked_prefill(const clv_prefill_args *a, clv_stream_t stream) {

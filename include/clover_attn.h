@@ -284,6 +284,19 @@ int clv_paged_decode_fp8(const clv_decode_args *args, const float *k_scales,
                          const float *v_scales, int32_t num_waves, void *workspace,
                          size_t workspace_bytes, clv_stream_t stream);
 
+/*
+ * First half of clv_paged_decode_fp8: the per-segment partials (normalised
+ * context, row maximum, row sum) into the workspace, for clv_balanced_reduce
+ * with the same arguments and the same explicit wave count to merge
+ * (num_waves <= 0 means clv_default_num_waves_fp8() here but
+ * clv_default_num_waves() in clv_balanced_reduce). For a caller that times the
+ * two kernels apart, or that merges partials from several GPUs of a
+ * context-parallel decode. No counterpart in the reference.
+ */
+int clv_paged_decode_fp8_partials(const clv_decode_args *args, const float *k_scales,
+                                  const float *v_scales, int32_t num_waves, void *workspace,
+                                  size_t workspace_bytes, clv_stream_t stream);
+
 /* Workspace bytes of clv_paged_decode_balanced (num_waves <= 0: default). */
 size_t clv_balanced_workspace_bytes(int32_t num_seqs, int32_t num_heads,
                                     int32_t num_kv_heads, int32_t head_dim,

@@ -118,3 +118,40 @@ def test_fp8_backend_steps():
             assert got.dtype == dt
             assert_attention_close(got, ref, what=f"step {step} layer {layer}")
     assert gpu.get_context_len("r") == cpu.get_context_len("r") == 32
+
+
+def test_fp8_partials_then_reduce_equal_the_one_call():
+    """clv_paged_decode_fp8_partials followed by clv_balanced_reduce (same
+    workspace and wave count) writes exactly what clv_paged_decode_fp8 writes."""
+    hq, hkv, d, bs = 28, 4, 128, 16
+    ctx = [1, 15, 16, 17, 0, 300, 1000, 33]
+    ks = torch.linspace(0.05, 3.0, hkv)
+    vs = torch.linspace(2.0, 0.1, hkv)
+    kc, vc, tables = _fp8_pools(hq + bs, ctx, hkv, d, bs, ks, vs)
+    q = torch.randn(len(ctx), hq, d, generator=torch.Generator().manual_seed(11)).to(torch.bfloat16)
+    q, kc, vc = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    bt = padded_tables(tables).to(DEV)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    ksd, vsd = ks.to(DEV), vs.to(DEV)
+    lib = kernels._native.load()
+    waves = lib.clv_default_num_waves_fp8()
+    outs = []
+    for split in (False, True):
+        out = torch.full(q.shape, float("nan"), dtype=q.dtype, device=DEV)
+        a = kernels.decode_args(out, q, kc, vc, bt, lens, bs, max(ctx))
+        ws = torch.empty(kernels.balanced_workspace_bytes(a, waves), dtype=torch.uint8, device=DEV)
+        stream = torch.cuda.current_stream().cuda_stream
+        if split:
+            kernels._native.check(lib.clv_paged_decode_fp8_partials(
+                a, ksd.data_ptr(), vsd.data_ptr(), waves, ws.data_ptr(), ws.numel(), stream),
+                "clv_paged_decode_fp8_partials")
+            kernels._native.check(lib.clv_balanced_reduce(a, waves, ws.data_ptr(), ws.numel(),
+                                                          stream), "clv_balanced_reduce")
+        else:
+            kernels._native.check(lib.clv_paged_decode_fp8(
+                a, ksd.data_ptr(), vsd.data_ptr(), waves, ws.data_ptr(), ws.numel(), stream),
+                "clv_paged_decode_fp8")
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1])
+    assert torch.isfinite(outs[0].float()).all()

@@ -265,6 +265,34 @@ def test_config_long_context_splitk_fp16():
         assert_north_star_bar(got, ref, f"long32k fp16, 2 x 32768, partition {partition}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d,max_ctx", [(32, 8, 128, 4096), (32, 8, 64, 4096),
+                                              (32, 1, 128, 8192)])
+def test_splitk_batch_equals_single_sequence_launches(dtype, hq, hkv, d, max_ctx):
+    """Split-K partials depend on nothing but their own (sequence, kv head,
+    partition): a batch of 16 ragged sequences (a grid of up to 16K
+    workgroups) and the same sequences launched one at a time give bitwise
+    equal outputs. Ragged contexts end on partial partitions, leave
+    workgroups past a short context idle and include an empty sequence; the
+    first rows are also checked against the oracle."""
+    ctx = [max_ctx, max_ctx - 1, max_ctx - 31, 3000, 33, 0, 1, max_ctx] * 2
+    print(f"split-K batch vs alone {dtype} hq={hq} hkv={hkv} d={d} max_ctx={max_ctx}", flush=True)
+    q, k, v, tables, scale = case(1100 + d + hkv, ctx, hq, hkv, d, 16, dtype)
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    bt = padded_tables(tables).to(DEV)
+    cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    batch = torch.full_like(qg, float("nan"))
+    kernels.paged_attention(batch, qg, kg, vg, bt, cl, 16, max_ctx, scale=scale, partition_size=32)
+    alone = torch.full_like(qg, float("nan"))
+    for s in range(len(ctx)):
+        kernels.paged_attention(alone[s:s + 1], qg[s:s + 1], kg, vg, bt[s:s + 1], cl[s:s + 1], 16,
+                                max_ctx, scale=scale, partition_size=32)
+    torch.cuda.synchronize()
+    assert torch.equal(batch.view(torch.int16), alone.view(torch.int16))
+    ref = oa.paged_decode(q[:2], k, v, tables[:2], ctx[:2], scale)
+    assert_attention_close(batch[:2].cpu(), ref, what="split-K batch vs oracle")
+
+
 def test_decode_repeated_calls_shared_workspace():
     """Ten calls of changing shapes, wave counts and dtypes on the same cached
     workspace, with split-K calls in between on the same stream: every result

@@ -392,6 +392,24 @@ int stream_depth_setting(int def) {
 static_assert(CLV_STREAM_RUN_COST >= 0 && CLV_STREAM_RUN_COST <= 64, "run cost 0..64 steps");
 constexpr int kStreamRunCost = CLV_STREAM_RUN_COST;
 
+// kv heads that one workgroup of the balanced decode reads together (one
+// wave each): all of them up to four (a token's whole row of the pools; GQA-7B
+// batch, 4 kv heads: 175.3 -> 173.1 us), else pairs (MHA Llama-7B batch, 32
+// kv heads: 329.0 -> 326.9 us with pairs, 336.4 with fours). A tuning build
+// may cap the group with the preprocessor value CLV_HEAD_GROUP_MAX.
+#ifndef CLV_HEAD_GROUP_MAX
+#define CLV_HEAD_GROUP_MAX 4
+#endif
+static_assert(CLV_HEAD_GROUP_MAX == 1 || CLV_HEAD_GROUP_MAX == 2 || CLV_HEAD_GROUP_MAX == 4,
+              "head group 1, 2 or 4");
+int head_group(int num_kv_heads, int num_waves) {
+  int hg = num_kv_heads <= 4 ? num_kv_heads : 2;
+  hg = std::min(hg, CLV_HEAD_GROUP_MAX);
+  if (hg == 3 || num_kv_heads % hg != 0) hg = 1;
+  while (hg > num_waves) hg /= 2;
+  return std::max(hg, 1);
+}
+
 // Validates a balanced-decode call and lays the workspace out in p.
 int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
                   size_t workspace_bytes, clv::DecodeParams *p) {
@@ -400,6 +418,7 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   if (num_waves <= 0) num_waves = clv_default_num_waves();
   if (num_waves > (1 << 22)) return CLV_EINVAL;
   const int64_t nseg = (int64_t)p->num_seqs * p->num_kv_heads * p->n_gchunks;
+  const int hg = head_group(p->num_kv_heads, num_waves);
   if (!clv::decode_stream_supported((DType)a->dtype, a->head_dim, a->block_size, nseg))
     return CLV_EUNSUPPORTED;
   if (p->num_seqs == 0) return CLV_OK;
@@ -410,10 +429,11 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   const size_t rows = ((size_t)num_waves + (size_t)nseg) * 16;
   char *ws = (char *)workspace;
   p->num_waves = num_waves;
+  p->head_group = hg;
   // fp32 steps are twice the bytes: two steps in flight (a sweep over 2-4).
   p->stream_depth = stream_depth_setting(a->dtype == CLV_F32 ? 2 : 3);
   p->stream_run_cost = kStreamRunCost;
-  p->num_segments = (int32_t)nseg;
+  p->num_segments = (int32_t)(nseg / hg);
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);
   p->ws_m = (float *)ws;

@@ -30,15 +30,17 @@ struct DecodeParams {
   float *ws_o;            // [num_seqs, num_heads, max_parts, head_dim] normalised contexts
   float *ws_m;            // [num_seqs, num_heads, max_parts] row max (natural-log domain)
   float *ws_l;            // [num_seqs, num_heads, max_parts] row sum
-  // Balanced (stream) mode: num_waves waves split the flattened
-  // (sequence, kv head, query-head chunk, 16-token step) space evenly; the
-  // workspace holds one partial per (segment, wave) pair, 16 rows each at
-  // row (segment + wave) * 16, in ws_o/ws_m/ws_l, plus the segment prefix
-  // sums written by workgroup 0.
+  // Balanced (stream) mode: groups of head_group waves (one workgroup's
+  // waves, one kv head each) split the flattened (sequence, kv-head group,
+  // query-head chunk, 16-token step) space evenly; the workspace holds one
+  // partial per (segment, group, kv head of the group), 16 rows each at row
+  // ((segment + group) * head_group + wave in group) * 16, in
+  // ws_o/ws_m/ws_l, plus the segment prefix sums written by workgroup 0.
   int32_t num_waves;
+  int32_t head_group;     // kv heads read together (1, 2 or 4; divides num_kv_heads)
   int32_t stream_depth;   // steps of loads each wave keeps in flight
   int32_t stream_run_cost;  // phantom steps charged for each segment start (see decode_stream.hip)
-  int32_t num_segments;   // num_seqs * num_kv_heads * n_gchunks
+  int32_t num_segments;   // num_seqs * (num_kv_heads / head_group) * n_gchunks
   int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
   // Fused append (balanced mode): when append_new is set, sequence s's new
   // key/value rows key_new/value_new[s] ([num_kv_heads, head_dim], strides in

@@ -20,6 +20,14 @@
 // steps. Segment i covers the flattened range [seg_prefix[i],
 // seg_prefix[i+1]), its real steps start stream_run_cost later.
 //
+// Head groups: the unit of the split is a group of head_group waves of one
+// workgroup (one SIMD each), which take the same steps of head_group
+// consecutive kv heads, one kv head per wave. The waves of a group then read
+// the rows of a token for all their kv heads at about the same time, as one
+// contiguous range of the block (a whole 16-token block of the GQA-7B pools
+// for head_group 4), which HBM serves faster than the same rows read at
+// unrelated times. A "segment" is then (sequence, kv-head group, chunk).
+//
 // Every workgroup derives the segment prefix sums itself (in LDS) from
 // context_lens; workgroup 0 also stores them for the reduce kernel.
 #include "decode_mfma.h"
@@ -91,7 +99,8 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   __shared__ int s_tmp[kWaves];
 
   const int nseg = p.num_segments;
-  const int per_seq = p.num_kv_heads * p.n_gchunks;
+  const int HG = p.head_group;
+  const int per_seq = (p.num_kv_heads / HG) * p.n_gchunks;
   const int K = p.stream_run_cost;
   for (int i = threadIdx.x; i < nseg; i += kThreads) {
     const int steps = (clamp_ctx(p, i / per_seq) + WV::STEP - 1) / WV::STEP;  // vector read
@@ -99,14 +108,16 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   }
   __syncthreads();
   const int64_t N = block_exclusive_scan(s_seg, nseg, s_tmp);
-  // At most one wave per step, so that every wave owns at least one step and
-  // each segment's partials come from consecutive waves.
-  const int64_t W = min((int64_t)p.num_waves, N);
+  // At most one group per step, so that every group owns at least one step
+  // and each segment's partials come from consecutive groups.
+  const int64_t W = min((int64_t)(p.num_waves / HG), N);
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= nseg; i += kThreads) seg_prefix[i] = s_seg[i];
   }
 
-  const int wid = (int)blockIdx.x * kWaves + uni(threadIdx.x >> 6);
+  const int wv = (int)blockIdx.x * kWaves + uni(threadIdx.x >> 6);
+  const int wid = wv / HG;      // group
+  const int wk = wv - wid * HG;  // kv head within the group
   if (N == 0 || wid >= W) return;
   const int st = span_start(wid, W, N);
   const int en = span_start(wid + 1, W, N);
@@ -137,7 +148,7 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
       const int lst = uni(s_seg[sg + 1]) - 1;
       if (lst < st || lst < uni(s_seg[sg]) + K) continue;  // not ours, or no real steps
       const int s_ = sg / per_seq;
-      const int kvh = sg - s_ * per_seq;  // one query-head chunk per kv head
+      const int kvh = (sg - s_ * per_seq) * HG + wk;  // one query-head chunk per kv head
       const int ctx = clamp_ctx(p, lens, s_);
       if (ctx != scalar_load_i32(lens + s_)) continue;  // the new position is not attended
       const SegGeom geo = seg_geom<T>(p, s_, kvh, ctx, tables);
@@ -170,8 +181,9 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     x = max(x, first);
     const int s_ = seg / per_seq;
     const int rem = seg - s_ * per_seq;
-    const int kvh = rem / p.n_gchunks;
-    const int g0 = (rem - kvh * p.n_gchunks) * 16;
+    const int kvg = rem / p.n_gchunks;
+    const int kvh = kvg * HG + wk;
+    const int g0 = (rem - kvg * p.n_gchunks) * 16;
     const int ng = min(16, p.group - g0);
     const int ctx = clamp_ctx(p, lens, s_);
     const SegGeom geo = seg_geom<T, CEB>(p, s_, kvh, ctx, tables);
@@ -225,11 +237,12 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
     }
 
     w.reduce_rowsum();
-    // Partial slot of the (segment, wave) pair: seg + wid. Along the
-    // flattened steps every change of segment or wave raises seg + wid, so
-    // the slots are distinct and fit the workspace's num_waves + nseg rows;
-    // the merge finds a segment's partials at seg + (its first wave) onwards.
-    const int64_t row0 = ((int64_t)seg + wid) * 16;
+    // Partial slot of the (segment, group) pair: seg + wid. Along the
+    // flattened steps every change of segment or group raises seg + wid, so
+    // the slots are distinct and below num_waves / HG + nseg; each holds HG
+    // partials of 16 rows (one per kv head of the group). The merge finds a
+    // segment's partials at slot seg + (its first group) onwards.
+    const int64_t row0 = (((int64_t)seg + wid) * HG + wk) * 16;
     w.store_partial(ws_o, ws_m, ws_l, row0, ng);
     w.reset();
     x = last + 1;
@@ -245,16 +258,19 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int h = (int)(idx - (int64_t)s * p.num_heads);
   const int kvh = h / p.group;
   const int gall = h - kvh * p.group;
-  const int seg = (s * p.num_kv_heads + kvh) * p.n_gchunks + gall / 16;
+  const int HG = p.head_group;
+  const int kvg = kvh / HG, wk = kvh - kvg * HG;
+  const int seg = (s * (p.num_kv_heads / HG) + kvg) * p.n_gchunks + gall / 16;
   const int g = gall % 16;
   const int a = p.seg_prefix[seg] + p.stream_run_cost, b = p.seg_prefix[seg + 1];
   const int64_t N = p.seg_prefix[p.num_segments];
-  const int64_t W = min((int64_t)p.num_waves, N);
+  const int64_t W = min((int64_t)(p.num_waves / HG), N);
   int n = 0;
   if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
-  const int64_t row0 = (n > 0 ? ((int64_t)seg + wave_of(a, W, N)) * 16 : 0) + g;
+  const int64_t row0 = (n > 0 ? (((int64_t)seg + wave_of(a, W, N)) * HG + wk) * 16 : 0) + g;
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
-  lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16, 16 * D, n, dst, nullptr);
+  lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
+                     dst, nullptr);
 }
 
 template <typename T, int D, int DEPTH>

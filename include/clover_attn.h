@@ -186,9 +186,11 @@ int clv_splitk_reduce(const clv_decode_args *args, int32_t partition_size,
 /*
  * Balanced decode for ragged batches (fp32/fp16/bf16, head_dim 64 or 128,
  * num_seqs * num_kv_heads * ceil(group/16) <= 4096): num_waves waves split
- * the batch's flattened 16-token steps evenly, crossing sequence borders;
- * each writes one partial per (sequence, kv head) it touches and a second
- * kernel merges them with the same log-sum-exp rule as the split-K reduce.
+ * the batch's flattened 16-token steps evenly, crossing sequence borders
+ * (in groups of up to four waves of one workgroup that take the same steps of
+ * adjacent kv heads); each writes one partial per (sequence, kv head) it
+ * touches and a second kernel merges them with the same log-sum-exp rule as
+ * the split-K reduce.
  * Same result as clv_paged_decode. num_waves <= 0 picks the device default
  * (clv_default_num_waves()). No counterpart kernel exists in the reference.
  */

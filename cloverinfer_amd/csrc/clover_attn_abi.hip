@@ -383,11 +383,12 @@ int stream_depth_setting(int def) {
 }
 
 // Phantom steps the balanced decode charges for each segment a wave starts
-// (a run start costs one memory latency, about two 16-token steps on MI355X:
-// measured per-wave durations grow by ~2.5 us per extra run). Fixed at build
-// time (preprocessor value CLV_STREAM_RUN_COST, default 2).
+// (a run start costs one memory latency: measured per-wave durations grow by
+// ~2.5 us per extra run). With head groups 4 measured best (GQA-7B batch:
+// 172.9 us at 2, 172.3 at 4, 173.5 at 6, 173.9 at 8). Fixed at build time
+// (preprocessor value CLV_STREAM_RUN_COST, default 4).
 #ifndef CLV_STREAM_RUN_COST
-#define CLV_STREAM_RUN_COST 2
+#define CLV_STREAM_RUN_COST 4
 #endif
 static_assert(CLV_STREAM_RUN_COST >= 0 && CLV_STREAM_RUN_COST <= 64, "run cost 0..64 steps");
 constexpr int kStreamRunCost = CLV_STREAM_RUN_COST;

@@ -50,11 +50,13 @@ struct OutDesc {
 // Split-K partials also record the row max in the natural-log domain and the
 // row sum, the (context, row_max, row_sum) triple of the reference's
 // partial-softmax segments (src/core/resident_kv_store.py:715-783).
+// `tid` numbers the NW * 64 threads that share the work (by default the
+// workgroup's; a wave that merges on its own passes its lane).
 template <typename T, int NW, int GR, int D>
 __device__ __forceinline__ void merge_and_store(const WaveSmem<NW, GR, D> &sm, int ng,
-                                                const OutDesc<T> &od) {
+                                                const OutDesc<T> &od, int tid = threadIdx.x) {
   constexpr int CPR = D / 8;  // 8-element chunks per row
-  for (int idx = threadIdx.x; idx < GR * CPR; idx += NW * 64) {
+  for (int idx = tid; idx < GR * CPR; idx += NW * 64) {
     const int g = idx / CPR;
     const int c = idx - g * CPR;
     if (g >= ng) continue;

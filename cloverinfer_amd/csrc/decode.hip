@@ -71,16 +71,25 @@ __device__ __forceinline__ OutDesc<T> out_desc(const DecodeParams &p, int s, int
 // The barrier's workgroup-scope release/acquire orders those stores before
 // every wave's loads (the waves of a workgroup share one CU's caches), and no
 // other workgroup reads the row.
-template <typename T, int D, int NW, bool UNI, bool APPEND = false>
-__global__ void __launch_bounds__(NW * 64)
+//
+// HG > 1 (split-K, NW = 1): the workgroup holds HG independent waves, wave w
+// taking kv head HG * (blockIdx.y / n_gchunks) + w over the same partition,
+// so that the rows of a token for HG adjacent kv heads are read together (one
+// contiguous range of the token's row in the pools).
+template <typename T, int D, int NW, bool UNI, bool APPEND = false, int HG = 1>
+__global__ void __launch_bounds__(NW * HG * 64)
 paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
+  static_assert(HG == 1 || (NW == 1 && !APPEND), "head groups: one wave per kv head");
   typedef typename GridWave<T, D, UNI>::type W;
-  __shared__ WaveSmem<NW, 16, D> sm;
+  __shared__ WaveSmem<NW, 16, D> sms[HG];
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hw = HG > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
+  WaveSmem<NW, 16, D> &sm = sms[hw];
+  const int wave = HG > 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int s = blockIdx.z;
-  const int kvh = blockIdx.y / p.n_gchunks;
-  const int g0 = (blockIdx.y - kvh * p.n_gchunks) * 16;
+  const int kvg = blockIdx.y / p.n_gchunks;
+  const int kvh = kvg * HG + hw;
+  const int g0 = (blockIdx.y - kvg * p.n_gchunks) * 16;
   const int ng = min(16, p.group - g0);
   const int h0 = kvh * p.group + g0;
 
@@ -180,7 +189,8 @@ paged_decode_mfma(const DecodeParams p, const int32_t *__restrict__ tables) {
     }
   }
   __syncthreads();
-  merge_and_store<T, NW, 16, D>(sm, ng, out_desc<T>(p, s, h0, blockIdx.x));
+  merge_and_store<T, NW, 16, D>(sm, ng, out_desc<T>(p, s, h0, blockIdx.x),
+                                HG > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x);
 }
 
 // ---------------------------------------------------------------- VALU kernel
@@ -226,16 +236,17 @@ __global__ void __launch_bounds__(256) splitk_reduce(const DecodeParams p) {
   lse_merge<T, D, 4>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 1, D, nparts, dst, smem);
 }
 
-template <typename T, int D, int NW, bool APPEND = false>
+template <typename T, int D, int NW, bool APPEND = false, int HG = 1>
 hipError_t launch_mfma_tdw(const DecodeParams &p, hipStream_t stream) {
+  if (p.num_kv_heads % HG != 0) return hipErrorInvalidValue;
   const dim3 grid(p.partition_size > 0 ? (unsigned)p.max_parts : 1u,
-                  (unsigned)(p.num_kv_heads * p.n_gchunks), (unsigned)p.num_seqs);
+                  (unsigned)(p.num_kv_heads / HG * p.n_gchunks), (unsigned)p.num_seqs);
   if (p.block_shift >= 4)
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true, APPEND>), grid, dim3(NW * 64), 0,
-                       stream, p, p.block_tables);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, true, APPEND, HG>), grid, dim3(NW * HG * 64),
+                       0, stream, p, p.block_tables);
   else
-    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false, APPEND>), grid, dim3(NW * 64), 0,
-                       stream, p, p.block_tables);
+    hipLaunchKernelGGL((paged_decode_mfma<T, D, NW, false, APPEND, HG>), grid,
+                       dim3(NW * HG * 64), 0, stream, p, p.block_tables);
   return hipGetLastError();
 }
 
@@ -254,9 +265,25 @@ hipError_t launch_mfma_append_t(const DecodeParams &p, hipStream_t stream) {
 // 16 x 32K-token fp16 365 / 358 / 358, the ragged GQA-7B bf16 batch
 // 286 / 274 / 270, the same over fp32 pools 574 / 511 / 484; 8 waves: 414
 // on the first).
+// Split-K workgroups hold a head group of four one-wave kv heads where the
+// kv-head count allows it (16 x 32K-token fp16, 8 kv heads, partition 512:
+// kernel 358.8 us with one kv head per workgroup, 364.9 with pairs, 341.5
+// with fours, 341.4 with eights). A tuning build may set the preprocessor
+// value CLV_SPLITK_HEAD_GROUP (1, 2, 4 or 8).
+#ifndef CLV_SPLITK_HEAD_GROUP
+#define CLV_SPLITK_HEAD_GROUP 4
+#endif
+static_assert(CLV_SPLITK_HEAD_GROUP == 1 || CLV_SPLITK_HEAD_GROUP == 2 ||
+                  CLV_SPLITK_HEAD_GROUP == 4 || CLV_SPLITK_HEAD_GROUP == 8,
+              "split-K head group 1, 2, 4 or 8");
 template <typename T, int D>
 hipError_t launch_mfma_td(const DecodeParams &p, hipStream_t stream) {
-  if (p.partition_size > 0) return launch_mfma_tdw<T, D, 1>(p, stream);
+  if (p.partition_size > 0) {
+    constexpr int HG = CLV_SPLITK_HEAD_GROUP;
+    if constexpr (HG > 1)
+      if (p.num_kv_heads % HG == 0) return launch_mfma_tdw<T, D, 1, false, HG>(p, stream);
+    return launch_mfma_tdw<T, D, 1>(p, stream);
+  }
   return launch_mfma_tdw<T, D, 4>(p, stream);
 }
 

@@ -664,35 +664,38 @@ struct StreamWave<float, D, UNI, false> {
 //   M = max_i m_i, w_i = l_i e^(m_i - M), out = sum_i c_i w_i / max(sum_i w_i, 1e-12).
 // Row i: row max m[i * ms] (natural-log domain), row sum l[i * ms], context
 // c[i * cs .. + D]. NW waves (consecutive in the workgroup, NW > 1 only for a
-// one-row workgroup) split the rows 64 at a time; each lane weighs one row of
-// a 64-row chunk, and eight context rows are loaded per round so that their
-// latencies overlap. NW > 1 combines the waves through smem (NW * (D + 1)
-// floats) and needs every thread of the workgroup to call this.
+// one-row workgroup) split the rows in chunks of C = min(64, ceil(n / NW));
+// each lane weighs one row of a chunk, and R context rows are loaded per
+// round so that their latencies overlap (R = 16 for NW > 1: 64 partitions
+// then take one round per wave). NW > 1 combines the waves through smem
+// (NW * (D + 1) floats) and needs every thread of the workgroup to call this.
 template <typename T, int D, int NW>
 __device__ __forceinline__ void lse_merge(const float *m, const float *l, const float *c,
                                           int64_t ms, int64_t cs, int n, T *dst, float *smem) {
   constexpr int EPL = (D + 63) / 64;
+  constexpr int R = NW > 1 ? 16 : 8;
   const int lane = threadIdx.x & 63;
   const int wv = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+  const int C = NW > 1 ? max(1, min(64, (n + NW - 1) / NW)) : 64;
   // The row's max needs every m_i; the first chunk's (m, l) and its first
-  // eight context rows are loaded together, before any reduction, so that a
-  // row with at most 64 partials costs one round trip to memory.
-  const int base0 = 64 * wv;
-  const int cnt0 = max(0, min(64, n - base0));
+  // R context rows are loaded together, before any reduction, so that a
+  // row with at most C * NW partials costs one round trip to memory.
+  const int base0 = C * wv;
+  const int cnt0 = max(0, min(C, n - base0));
   float m0 = kNegInf, l0 = 0.f;
   if (lane < cnt0) {
     m0 = m[(int64_t)(base0 + lane) * ms];
     l0 = l[(int64_t)(base0 + lane) * ms];
   }
-  float v[8][EPL];
+  float v[R][EPL];
 #pragma unroll
-  for (int u = 0; u < 8; ++u)
+  for (int u = 0; u < R; ++u)
 #pragma unroll
     for (int e = 0; e < EPL; ++e)
       v[u][e] = (u < cnt0 && lane + 64 * e < D) ? c[(int64_t)(base0 + u) * cs + lane + 64 * e] : 0.f;
   float M = m0;
   for (int i = lane; i < n; i += 64)
-    if (i < base0 || i >= base0 + 64) M = fmaxf(M, m[i * ms]);
+    if (i < base0 || i >= base0 + cnt0) M = fmaxf(M, m[i * ms]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
   const float Msub = (M == kNegInf) ? 0.f : M;
@@ -700,8 +703,8 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int base = base0; base < n; base += 64 * NW) {
-    const int cnt = min(64, n - base);
+  for (int base = base0; base < n; base += C * NW) {
+    const int cnt = min(C, n - base);
     float wl = 0.f;
     if (base == base0) {
       if (lane < cnt) wl = l0 * fast_exp2((m0 - Msub) * kLog2e);
@@ -710,17 +713,17 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
       wl = l[r] * fast_exp2((m[r] - Msub) * kLog2e);
     }
     L += wl;
-    for (int k = 0; k < cnt; k += 8) {
+    for (int k = 0; k < cnt; k += R) {
       if (base != base0 || k != 0) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < R; ++u)
 #pragma unroll
           for (int e = 0; e < EPL; ++e)
             v[u][e] = (k + u < cnt && lane + 64 * e < D)
                           ? c[(int64_t)(base + k + u) * cs + lane + 64 * e] : 0.f;
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < R; ++u) {
         const float w = __builtin_bit_cast(
             float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), k + u < 64 ? k + u : 63));
 #pragma unroll

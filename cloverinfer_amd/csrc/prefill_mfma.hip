@@ -75,20 +75,14 @@ __device__ __forceinline__ u32x4 vt_read(uint32_t lo, uint32_t hi) {
   return (u32x4){ua[0], ua[1], ub[0], ub[1]};
 }
 
-// Two bf16 values (one 32-bit word) as two fp16 values. `hmax` collects the
-// largest fp16 magnitude bits of each half (packed unsigned 16-bit maxima):
-// a half at or above 0x7c00 is an fp16 infinity or NaN, i.e. a bf16 value
-// that did not fit (magnitude >= 65520 rounds to infinity) or a NaN.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w, uint32_t &hmax) {
+// Two bf16 values (one 32-bit word) as two fp16 values (round to nearest
+// even; a magnitude of 65520 or more becomes an fp16 infinity).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
   typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
   const float a = __builtin_bit_cast(float, w << 16);
   const float b = __builtin_bit_cast(float, w & 0xffff0000u);
-  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
-  hmax = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, hmax),
-                                                                __builtin_bit_cast(u16x2, h & 0x7fff7fffu)));
-  return h;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
 }
 
 template <typename T, int D>
@@ -233,10 +227,9 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     }
   };
   // Stage the loaded rows into LDS buffer buf. The fast pass stores V as
-  // fp16 and flags values that do not fit; the exact pass stores V as is.
+  // fp16; the exact pass stores V as is.
   auto store_tile = [&](int buf, auto exact_c) {
     constexpr bool EXACT = decltype(exact_c)::value;
-    uint32_t hmax = 0u;
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int row = lrow + RPP * i;
@@ -244,12 +237,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       u32x4 v = vreg[i];
       if constexpr (kBf16 && !EXACT) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e], hmax);
+        for (int e = 0; e < 4; ++e) v[e] = bf16x2_to_f16x2(v[e]);
       }
       store_vec<u32x4>(&sV[buf][row * VROW + lchunk * 8], v);
       if (lchunk == 0) sValid[buf][row] = rvalid[i] ? 1 : 0;
     }
-    if (kBf16 && !EXACT && ((hmax & 0xffffu) >= 0x7c00u || (hmax >> 16) >= 0x7c00u)) sOvf = 1;
   };
 
   f32x4 o[kRT][CH];
@@ -497,6 +489,20 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
     if (ntiles > 0) {
       if (lag) softmax_step(2 * ntiles - 1, full_prev);
       pv(2 * ntiles - 1);
+    }
+    if constexpr (kBf16 && !EXACT) {
+      // A bf16 V value that did not fit fp16 became an infinity (or was
+      // one, or a NaN): every P.V product of its half-step then made the
+      // accumulators of all rows of every wave infinite or NaN (0 * inf
+      // included), so a non-finite accumulator of any wave flags it.
+      float acc = 0.f;
+#pragma unroll
+      for (int rt = 0; rt < kRT; ++rt)
+#pragma unroll
+        for (int m = 0; m < CH; ++m)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc += o[rt][m][e] * 0.f;
+      if (__any(acc != 0.f)) sOvf = 1;  // x * 0 is 0 for every finite x
     }
     __syncthreads();  // sOvf final; LDS free for a second pass
     return kBf16 && !EXACT && sOvf != 0;

@@ -79,12 +79,12 @@ def padded_tables(tables, width: int | None = None) -> torch.Tensor:
 # benchmark workloads: max-abs 2e-3 against the fp32 oracle everywhere, and
 # max-rel 1e-2 where |ref| >= 0.2 (a relative bound on near-zero outputs is
 # ill-posed: a 16-bit output of 1e-4 is rounded by more than 1 % of itself).
-NS_ATOL = 2e-3
-NS_RTOL = 1e-2
-NS_REL_FLOOR = 0.2
+PARITY_ATOL = 2e-3
+PARITY_RTOL = 1e-2
+PARITY_REL_FLOOR = 0.2
 
 
-def assert_north_star_bar(got: torch.Tensor, ref: torch.Tensor, what: str) -> dict:
+def assert_parity_bar(got: torch.Tensor, ref: torch.Tensor, what: str) -> dict:
     """Assert max-abs <= 2e-3 and max-rel <= 1e-2 (where |ref| >= 0.2);
     print the observed margins and, when CLV_PARITY_LOG names a file, append
     them to it as a JSON line. Returns the figures."""
@@ -96,7 +96,7 @@ def assert_north_star_bar(got: torch.Tensor, ref: torch.Tensor, what: str) -> di
     assert got.shape == ref.shape, f"{what}: shape {tuple(got.shape)} != {tuple(ref.shape)}"
     assert torch.isfinite(got).all(), f"{what}: non-finite output"
     err = (got - ref).abs()
-    big = ref.abs() >= NS_REL_FLOOR
+    big = ref.abs() >= PARITY_REL_FLOOR
     rec = {
         "what": what,
         "elements": err.numel(),
@@ -106,13 +106,13 @@ def assert_north_star_bar(got: torch.Tensor, ref: torch.Tensor, what: str) -> di
         "rel_elements": int(big.sum()),
         "max_abs_ref": ref.abs().max().item(),
     }
-    print(f"[parity] {what}: max-abs {rec['max_abs']:.3e} (bar {NS_ATOL:g}), max-rel "
+    print(f"[parity] {what}: max-abs {rec['max_abs']:.3e} (bar {PARITY_ATOL:g}), max-rel "
           f"{rec['max_rel']:.3e} over {rec['rel_elements']} elements with |ref| >= "
-          f"{NS_REL_FLOOR:g} (bar {NS_RTOL:g}); max |ref| {rec['max_abs_ref']:.3f}", flush=True)
+          f"{PARITY_REL_FLOOR:g} (bar {PARITY_RTOL:g}); max |ref| {rec['max_abs_ref']:.3f}", flush=True)
     path = os.environ.get("CLV_PARITY_LOG")
     if path:
         with open(path, "a") as f:
             f.write(json.dumps(rec) + "\n")
-    assert rec["max_abs"] <= NS_ATOL, f"{what}: max-abs {rec['max_abs']:.3e} > {NS_ATOL:g}"
-    assert rec["max_rel"] <= NS_RTOL, f"{what}: max-rel {rec['max_rel']:.3e} > {NS_RTOL:g}"
+    assert rec["max_abs"] <= PARITY_ATOL, f"{what}: max-abs {rec['max_abs']:.3e} > {PARITY_ATOL:g}"
+    assert rec["max_rel"] <= PARITY_RTOL, f"{what}: max-rel {rec['max_rel']:.3e} > {PARITY_RTOL:g}"
     return rec

@@ -10,7 +10,7 @@ import torch
 from cloverinfer_amd import kernels
 from cloverinfer_amd.memory_manager import KVCacheManager
 from oracle import attention as oa
-from tests.helpers import (assert_attention_close, assert_north_star_bar, make_paged_kv,
+from tests.helpers import (assert_attention_close, assert_parity_bar, make_paged_kv,
                            padded_tables)
 
 pytestmark = pytest.mark.gpu
@@ -227,7 +227,7 @@ def test_config_opt125m_fp32_with_append():
     torch.cuda.synchronize()
     ref = torch.stack([oa.attend(q[i], kv[r][0], kv[r][1], 1 / 8) for i, r in enumerate(rids)])
     assert_attention_close(out.cpu(), ref, atol=1e-4, rtol=1e-4)
-    assert_north_star_bar(out, ref, "opt125m fp32, 8 x 128 (full config)")
+    assert_parity_bar(out, ref, "opt125m fp32, 8 x 128 (full config)")
 
 
 @pytest.mark.parametrize("nseq", [8])
@@ -238,7 +238,7 @@ def test_config_llama7b_mha_fp16(nseq):
     for partition in (None, 0, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"llama7b P{partition}")
-        assert_north_star_bar(got, ref, f"llama7b fp16, {nseq} x 2048, partition {partition}")
+        assert_parity_bar(got, ref, f"llama7b fp16, {nseq} x 2048, partition {partition}")
 
 
 def test_config_qwen7b_gqa_bf16_ragged():
@@ -249,10 +249,10 @@ def test_config_qwen7b_gqa_bf16_ragged():
     for partition in (None, 0, 256, 512):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"qwen7b P{partition}")
-        assert_north_star_bar(got, ref, f"qwen7b bf16, 16 seqs U[256,8192], partition {partition}")
+        assert_parity_bar(got, ref, f"qwen7b bf16, 16 seqs U[256,8192], partition {partition}")
     got = run_decode(q, k, v, tables, ctx, scale, num_waves=37)
     assert_attention_close(got, ref, what="qwen7b balanced W=37")
-    assert_north_star_bar(got, ref, "qwen7b bf16, 16 seqs, balanced W=37")
+    assert_parity_bar(got, ref, "qwen7b bf16, 16 seqs, balanced W=37")
 
 
 def test_config_long_context_splitk_fp16():
@@ -262,7 +262,7 @@ def test_config_long_context_splitk_fp16():
     for partition in (512, None):
         got = run_decode(q, k, v, tables, ctx, scale, partition_size=partition)
         assert_attention_close(got, ref, what=f"long-context P{partition}")
-        assert_north_star_bar(got, ref, f"long32k fp16, 2 x 32768, partition {partition}")
+        assert_parity_bar(got, ref, f"long32k fp16, 2 x 32768, partition {partition}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

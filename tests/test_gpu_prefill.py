@@ -9,7 +9,7 @@ import torch
 
 from cloverinfer_amd import kernels
 from oracle import attention as oa
-from tests.helpers import (assert_attention_close, assert_north_star_bar, make_paged_kv,
+from tests.helpers import (assert_attention_close, assert_parity_bar, make_paged_kv,
                            padded_tables)
 
 pytestmark = pytest.mark.gpu
@@ -67,7 +67,7 @@ def test_prefill_reduced_chunk_config():
     got = run_prefill(q, k, v, tables, ctx, qsl, scale)
     ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
     assert_attention_close(got, ref, what="chunked prefill 4096+512")
-    assert_north_star_bar(got, ref, "prefill bf16, 2 x (4096 + 512), successive-step oracle")
+    assert_parity_bar(got, ref, "prefill bf16, 2 x (4096 + 512), successive-step oracle")
 
 
 def test_prefill_full_config_against_masked_oracle():
@@ -84,7 +84,7 @@ def test_prefill_full_config_against_masked_oracle():
         refs.append(oa.chunked_prefill_masked(q[qsl[s]:qsl[s + 1]], kk, vv, scale))
     ref = torch.cat(refs)
     assert_attention_close(got, ref, what="chunked prefill 8 x (4096+512)")
-    assert_north_star_bar(got, ref, "prefill bf16, 8 x (4096 + 512) (full config)")
+    assert_parity_bar(got, ref, "prefill bf16, 8 x (4096 + 512) (full config)")
 
 
 def test_prefill_rows_equal_decode_steps_full_config():

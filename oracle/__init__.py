@@ -12,8 +12,8 @@ this repository's kernels must reproduce:
   (src/core/memory_manager.py:55-173).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker or as the
-timed CPU baseline. The product package ``cloverinfer_amd`` never imports it.
+``bench.py`` may import this package, and only as the reference results a
+test compares against or as the timed CPU baseline. The product package ``cloverinfer_amd`` never imports it.
 
 Every function is pinned by checks in tests/test_oracle.py that do not
 retype its formula: the reference tests' known answers

@@ -9,10 +9,11 @@
 // einsum/softmax/einsum (src/core/attention_backend.py:116-118).
 //
 // Work decomposition: one workgroup per (sequence, kv head, query-head chunk
-// of <= 16, partition). The query heads that share a kv head are packed, so
-// every K/V byte is read from HBM once per kv head. The partition is the
-// whole context (single pass) or partition_size tokens (split-K, followed by
-// splitk_reduce).
+// of <= 16, partition); split-K workgroups hold up to four of those, adjacent
+// kv heads over the same partition, one wave each. The query heads that share
+// a kv head are packed, so every K/V byte is read from HBM once per kv head.
+// The partition is the whole context (single pass) or partition_size tokens
+// (split-K, followed by splitk_reduce).
 //
 // fp16/bf16 use MFMA (v_mfma_f32_16x16x32_*): per 32-token step a wave runs
 //   S^T[t, g]  = K[t, :] . Q[g, :]           (2 x D/32 MFMAs, K straight from HBM)

@@ -338,11 +338,76 @@ def cpu_baseline_prefill(host, budget_s: float):
     }
 
 
-def roofline(bound: str, kernel: str, achieved: float, traffic, traffic_note):
+# How the roofline's kernel time is taken, for every workload: K launches of
+# the dominant kernel alone, queued back to back on its stream between one
+# pair of HIP events, total / K (time_steps' ``solo`` figure). It agrees with
+# rocprofv3's per-dispatch average; per-launch event pairs add a launch gap
+# to every launch and are reported beside it, never used for ``frac``.
+ROOFLINE_TIMING = ("back-to-back mean: K launches of the kernel alone between one pair of HIP "
+                   "events on its stream, total / K")
+
+
+def roofline(bound: str, kernel: str, work: float, kernel_us: float, traffic, traffic_note):
+    """``work``: algorithmic bytes (hbm) or flops (mfma) per launch;
+    ``kernel_us``: the back-to-back mean launch time."""
     peak = PEAK_HBM_GBS if bound == "hbm" else PEAK_BF16_TFLOPS
+    achieved = work / (kernel_us * 1e-6) / (1e9 if bound == "hbm" else 1e12)
     return {"bound": bound, "kernel": kernel, "achieved": achieved, "peak": peak,
             "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": achieved / peak,
+            "kernel_us": kernel_us, "work_per_launch": work, "timing": ROOFLINE_TIMING,
             "traffic": traffic, "traffic_source": traffic_note}
+
+
+# Parity bar of the attention outputs against the fp32 oracle, as in the
+# tests: max-abs <= 2e-3 everywhere and max-rel <= 1e-2 where |ref| >= 0.2.
+PARITY_ATOL, PARITY_RTOL, PARITY_REL_FLOOR = 2e-3, 1e-2, 0.2
+
+
+def parity_record(got, ref, rows: int, what: str) -> dict:
+    """Margins of a timed launch's output ``got`` against the oracle's
+    ``ref`` (same shape, any float dtype) and whether they meet the bar."""
+    import torch
+
+    got = got.float()
+    ref = ref.float()
+    finite = bool(torch.isfinite(got).all())
+    err = (got - ref).abs()
+    big = ref.abs() >= PARITY_REL_FLOOR
+    max_abs = float(err.max()) if err.numel() else 0.0
+    max_rel = float((err[big] / ref.abs()[big]).max()) if bool(big.any()) else 0.0
+    return {"what": what, "rows": rows, "elements": err.numel(), "max_abs": max_abs,
+            "max_rel": max_rel, "rel_elements": int(big.sum()), "finite": finite,
+            "bar": {"max_abs": PARITY_ATOL, "max_rel": PARITY_RTOL,
+                    "rel_where_abs_ref_at_least": PARITY_REL_FLOOR},
+            "within_bar": finite and max_abs <= PARITY_ATOL and max_rel <= PARITY_RTOL}
+
+
+def decode_reference(host):
+    """The oracle's fp32 decode output for every sequence of the batch."""
+    import torch
+    from oracle import attention as oa
+
+    return torch.stack([oa.attend(qi, kk, vv, host["scale"]) for qi, kk, vv in host["seqs"]])
+
+
+def parity_decode(host, what: str) -> dict:
+    return parity_record(host["out"], decode_reference(host), len(host["seqs"]), what)
+
+
+def prefill_reference(host):
+    """The oracle's fp32 chunked-prefill output ``[S, new, Hq, D]`` (one
+    causal-masked contraction per sequence)."""
+    import torch
+    from oracle import attention as oa
+
+    return torch.stack([oa.chunked_prefill_masked(host["q"][s], host["keys"][s],
+                                                  host["values"][s], host["scale"])
+                        for s in range(host["q"].shape[0])])
+
+
+def parity_prefill(host, what: str) -> dict:
+    q = host["q"]
+    return parity_record(host["out"], prefill_reference(host), q.shape[0] * q.shape[1], what)
 
 
 def measure_decode(args, name):
@@ -456,9 +521,11 @@ def measure_decode(args, name):
         f"{part if mode == 'split' else 0}, {copies} pool copies)")
     dom = names.index("paged_decode_append" if fused is not None else "paged_decode")
     ms, ev, dec_batched = time_steps(args, phases, solo=dom)
-    # The roofline's kernel time: the smaller of the per-launch event mean and
-    # the back-to-back figure (see time_steps).
-    dec_us = min(ev[dom][0], dec_batched)
+    # Every step computes the same output from the same inputs (the pool
+    # copies are equal, the append rewrites one row with the same data): the
+    # last timed launch's output is what the parity leg checks.
+    torch.cuda.synchronize()
+    out_host = out.cpu()
     log(f"{name}: step {ms:.4f} ms, " + ", ".join(f"{n} {e[0]:.1f} us" for n, e in zip(names, ev)))
     step_bytes = w["algo_bytes"] + append_bytes
     kernel = {"balanced": "paged_decode_stream", "split": "paged_decode_mfma (split-K partials)",
@@ -483,7 +550,7 @@ def measure_decode(args, name):
         "kernels_us": {n: e[0] for n, e in zip(names, ev)},
         "kernels_us_median": {n: e[1] for n, e in zip(names, ev)},
         "kernel_us_back_to_back": {names[dom]: dec_batched},
-        "roofline": roofline("hbm", kernel, kernel_bytes / (dec_us * 1e-6) / 1e9, traffic, note),
+        "roofline": roofline("hbm", kernel, kernel_bytes, dec_batched, traffic, note),
     }
     if two_launch is not None:
         entry["two_launch"] = two_launch
@@ -496,7 +563,8 @@ def measure_decode(args, name):
     for i, c in enumerate(w["ctx"]):
         kk, vv = oa.gather_context(kc, vc, w["table_host"][i].tolist(), c)
         seqs.append((q[i], kk.contiguous(), vv.contiguous()))
-    host = {"seqs": seqs, "eb": w["eb"], "dtype": w["dtype"], "scale": w["scale"]}
+    host = {"seqs": seqs, "eb": w["eb"], "dtype": w["dtype"], "scale": w["scale"],
+            "out": out_host}
     del pools, args_list, w
     torch.cuda.empty_cache()
     return entry, host
@@ -547,6 +615,8 @@ def measure_prefill(args):
     log(f"prefill: warmup {args.warmup}, {args.steps} steps")
     ms, ev, att_batched = time_steps(args, [append, attend], solo=1)
     (app_us, app_med), (att_us, att_med) = ev
+    torch.cuda.synchronize()
+    out_host = out.cpu().view(S, new, hq, d)
     log(f"prefill: step {ms:.4f} ms, append {app_us:.1f} us, prefill {att_us:.1f} us")
     flops = 4 * d * hq * S * sum(cached + i + 1 for i in range(new))
     traffic, note = traffic_for("prefill")
@@ -562,8 +632,7 @@ def measure_prefill(args):
         "kernels_us": {"reshape_and_cache": app_us, "chunked_prefill": att_us},
         "kernels_us_median": {"reshape_and_cache": app_med, "chunked_prefill": att_med},
         "kernel_us_back_to_back": {"chunked_prefill": att_batched},
-        "roofline": roofline("mfma", "chunked_prefill_mfma",
-                             flops / (min(att_us, att_batched) * 1e-6) / 1e12, traffic, note),
+        "roofline": roofline("mfma", "chunked_prefill_mfma", flops, att_batched, traffic, note),
     }
     # Host copies for the CPU baseline: each sequence's whole context in the
     # reference backend's contiguous form, the query rows per sequence.
@@ -576,7 +645,7 @@ def measure_prefill(args):
         keys.append(kk.contiguous())
         values.append(vv.contiguous())
     host = {"q": q.cpu().view(S, new, hq, d), "keys": keys, "values": values, "new": new,
-            "scale": scale, "dtype": torch.bfloat16}
+            "scale": scale, "dtype": torch.bfloat16, "out": out_host}
     del k, v, q, kn, vn, out
     torch.cuda.empty_cache()
     return entry, host
@@ -598,6 +667,15 @@ def bench_all(args, names):
                 entry["cpu_baseline"] = cpu_baseline_prefill(host, budget)
             else:
                 entry["cpu_baseline"] = cpu_baseline_decode(host, budget)
+    for name in names:
+        entry, host = measured[name]
+        log(f"{name}: parity of the timed launch's output against the oracle")
+        what = f"{name}: last timed launch, every row"
+        entry["parity"] = (parity_prefill(host, what) if name == "prefill"
+                           else parity_decode(host, what))
+        p = entry["parity"]
+        log(f"{name}: parity max-abs {p['max_abs']:.3e}, max-rel {p['max_rel']:.3e} over "
+            f"{p['rows']} rows: {'within' if p['within_bar'] else 'OUTSIDE'} the bar")
     return {n: measured[n][0] for n in names}
 
 
@@ -630,6 +708,8 @@ def result_line(args, entries, head: str):
         res["hbm_frac_of_peak"] = e["value"] / PEAK_HBM_GBS
     if "cpu_baseline" in e:
         res["cpu_baseline"] = e["cpu_baseline"]
+    if "parity" in e:
+        res["parity"] = e["parity"]
     if len(entries) > 1:
         res["configs"] = entries
     res["gpu_clock_settle_s"] = args.settle
@@ -677,6 +757,8 @@ def bench_decode_fp8(args):
 
     ms, ev, dec_batched = time_steps(args, [partials, merge], solo=0)
     call_us, call_med = ev[0]
+    torch.cuda.synchronize()
+    out_host = out.cpu()
     ctx = w["ctx"]
     kv_bytes = sum(ctx) * cfg["hkv"] * cfg["d"] * 1 * 2
     qo_bytes = len(ctx) * cfg["hq"] * cfg["d"] * 2 * 2
@@ -685,6 +767,20 @@ def bench_decode_fp8(args):
     merge_us, merge_med = ev[1]
     log(f"step {ms:.4f} ms, decode {call_us:.1f} us, merge {merge_us:.1f} us")
     traffic, note = traffic_for("qwen7b_fp8")
+    # Parity of the last timed launch: the oracle over the dequantised pools
+    # (scale 1: each code's e4m3 value), every sequence.
+    from oracle import attention as oa
+
+    log("qwen7b_fp8: parity of the timed launch's output against the oracle")
+    kc, vc, q = k8.cpu().float(), v8.cpu().float(), w["q"].cpu()
+    seqs = []
+    for i, c in enumerate(ctx):
+        kk, vv = oa.gather_context(kc, vc, w["table_host"][i].tolist(), c)
+        seqs.append((q[i], kk, vv))
+    parity = parity_decode({"seqs": seqs, "scale": w["scale"], "out": out_host},
+                           "qwen7b_fp8: last timed launch, every row")
+    log(f"qwen7b_fp8: parity max-abs {parity['max_abs']:.3e}: "
+        f"{'within' if parity['within_bar'] else 'OUTSIDE'} the bar")
     return {
         "metric": "decode-attn HBM GB/s, fp8 KV pools, GQA-7B shape, 1 GPU",
         "value": algo / (ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -700,8 +796,8 @@ def bench_decode_fp8(args):
         "kernels_us": {"paged_decode": call_us, "merge": merge_us},
         "kernels_us_median": {"paged_decode": call_med, "merge": merge_med},
         "kernel_us_back_to_back": {"paged_decode": dec_batched},
-        "roofline": roofline("hbm", "paged_decode_stream (fp8)",
-                             algo / (min(call_us, dec_batched) * 1e-6) / 1e9, traffic, note),
+        "roofline": roofline("hbm", "paged_decode_stream (fp8)", algo, dec_batched, traffic, note),
+        "parity": parity,
     }
 
 
@@ -830,6 +926,13 @@ def main() -> int:
     else:
         result = bench_node(args, packed=True)
     print(json.dumps(result), flush=True)
+    # A timed launch whose output is outside the parity bar fails the run.
+    bad = [n for n, e in (result.get("configs") or {"": result}).items()
+           if "parity" in e and not e["parity"]["within_bar"]]
+    if bad:
+        print(f"bench.py: output outside the parity bar for {', '.join(bad) or result['metric']}",
+              file=sys.stderr)
+        return 3
     return 0
 
 

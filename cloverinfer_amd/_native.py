@@ -177,7 +177,9 @@ _lib: ctypes.CDLL | None = None
 
 
 def library_path() -> str:
-    return _build.LIB_PATH
+    """The in-tree library, or the file ``CLV_LIB_PATH`` names (the
+    host-sanitized build, see cloverinfer_amd/build.py)."""
+    return os.environ.get("CLV_LIB_PATH") or _build.LIB_PATH
 
 
 def load() -> ctypes.CDLL:

@@ -117,10 +117,16 @@ class GpuAttentionBackend:
         self._bshift = block_size.bit_length() - 1
         self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
         self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
-        # Device-side twins of the staging buffer and of the output, reused by
-        # every wave whose results go back to the host (such a call waits for
-        # them before it returns), and the fused launches built for them.
+        # Device twin of the staging buffer, reused by every wave: a wave
+        # whose results stay on the device returns while its kernels may still
+        # read it, so the next wave's upload into it is ordered after them
+        # (stream order on the same stream, an event wait across streams).
+        # The device output buffer serves only waves whose results go back to
+        # the host (such a call waits for them before it returns). And the
+        # fused launches built for the staged views.
         self._dstage: Optional[torch.Tensor] = None
+        self._dstage_free: Optional[torch.cuda.Event] = None  # after the last reader of _dstage
+        self._dstage_stream: Optional[int] = None  # stream of that reader
         self._dout: Optional[torch.Tensor] = None
         self._launches: Dict[tuple, "kernels.AppendDecodeLaunch"] = {}
         self._views: Dict[tuple, tuple] = {}  # device views into _dstage per batch shape
@@ -517,14 +523,18 @@ class GpuAttentionBackend:
                 flat, blocks = self.tables.flat_updates(upd)
                 buf[o_u:o_u + 8 * nu].numpy().view(np.int64)[:] = flat
                 buf[o_u + 8 * nu:total].numpy().view(np.int32)[:] = blocks
+            stream = torch.cuda.current_stream(self.device)
+            if self._dstage_free is not None and self._dstage_stream != stream.cuda_stream:
+                stream.wait_event(self._dstage_free)  # the previous wave's kernels read it
             if self._dstage is None or self._dstage.numel() < total:
                 self._dstage = torch.empty(max(2 * total, 1 << 20), dtype=torch.uint8,
                                            device=self.device)
                 self._views.clear()
             dev = self._dstage[:total]
             dev.copy_(buf[:total], non_blocking=True)
-            self._stage_done = torch.cuda.Event()
-            self._stage_done.record()
+            if self._stage_done is None:
+                self._stage_done = torch.cuda.Event()
+            self._stage_done.record(stream)
             vkey = (n, hq, hkv, d, dt, kdt)
             views = self._views.get(vkey)
             if views is None:
@@ -586,6 +596,10 @@ class GpuAttentionBackend:
             if not applied:
                 self.tables.requeue(upd)
             raise
+        if self._dstage_free is None:
+            self._dstage_free = torch.cuda.Event()
+        self._dstage_free.record(stream)
+        self._dstage_stream = stream.cuda_stream
         if layer == self.num_layers - 1:
             self._ctx[rows] += 1
         self.stats["decode_items"] += n

@@ -6,6 +6,17 @@ root, the library to ``cloverinfer_amd/_lib/`` (both git-ignored; the library
 travels with the source tree to the machine that runs it).
 
 Run ``python -m cloverinfer_amd.build`` or call :func:`build`.
+
+``python -m cloverinfer_amd.build --sanitize`` builds a second copy whose host
+code (the C ABI's validation, sizing and launch set-up) is compiled with
+AddressSanitizer and UndefinedBehaviorSanitizer, into ``_lib/sanitize/``
+(objects in ``_build/sanitize/``); the device code is built as usual.
+``CLV_LIB_PATH`` points the loader at it, and the process must preload the
+sanitizer runtime (:func:`sanitizer_runtime`), e.g.::
+
+    LD_PRELOAD=$(python -m cloverinfer_amd.build --print-asan-runtime) \
+    ASAN_OPTIONS=detect_leaks=0 CLV_LIB_PATH=cloverinfer_amd/_lib/sanitize/libclover_attn.so \
+    python -m pytest tests/test_abi.py tests/test_blocks.py
 """
 from __future__ import annotations
 
@@ -34,6 +45,14 @@ SOURCES = [
 ]
 
 ARCH = "gfx950"
+
+SANITIZE_LIB_PATH = os.path.join(LIB_DIR, "sanitize", LIB_NAME)
+# Host-only sanitizer flags: each one behind -Xarch_host, so that the gfx950
+# device code is compiled exactly as in the normal build.
+SANITIZE_FLAGS = [f for flag in ("-fsanitize=address", "-fsanitize=undefined",
+                                 "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer",
+                                 "-g")
+                  for f in ("-Xarch_host", flag)]
 
 
 def _hipcc() -> str:
@@ -64,9 +83,11 @@ def compile_flags() -> list[str]:
     ]
 
 
-def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *compile_flags(), "-c", os.path.join(CSRC_DIR, src), "-o", obj]
+def _compile(src: str, verbose: bool, sanitize: bool = False) -> str:
+    out_dir = os.path.join(BUILD_DIR, "sanitize") if sanitize else BUILD_DIR
+    obj = os.path.join(out_dir, os.path.splitext(src)[0] + ".o")
+    cmd = [_hipcc(), *compile_flags(), *(SANITIZE_FLAGS if sanitize else []), "-c",
+           os.path.join(CSRC_DIR, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -80,24 +101,47 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every source for gfx950 and link ``libclover_attn.so``; returns its path."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    os.makedirs(LIB_DIR, exist_ok=True)
+def build(verbose: bool = False, jobs: int | None = None, sanitize: bool = False) -> str:
+    """Compile every source for gfx950 and link ``libclover_attn.so``; returns
+    its path. ``sanitize``: the host-sanitized copy at SANITIZE_LIB_PATH."""
+    lib_path = SANITIZE_LIB_PATH if sanitize else LIB_PATH
+    os.makedirs(os.path.join(BUILD_DIR, "sanitize") if sanitize else BUILD_DIR, exist_ok=True)
+    os.makedirs(os.path.dirname(lib_path), exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, verbose, sanitize), SOURCES))
+    tmp = lib_path + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    if sanitize:
+        # The runtime itself comes from the preloaded shared library.
+        cmd += ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                "-shared-libasan"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
+
+
+def sanitizer_runtime() -> str:
+    """Path of the AddressSanitizer runtime (which carries the
+    UndefinedBehaviorSanitizer checks too) that a process loading the
+    sanitized library must preload."""
+    res = subprocess.run([_hipcc(), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                         capture_output=True, text=True)
+    path = res.stdout.strip()
+    if res.returncode != 0 or not os.path.isabs(path) or not os.path.exists(path):
+        llvm = os.path.join(os.path.dirname(os.path.realpath(_hipcc())), "..", "llvm")
+        raise RuntimeError(f"AddressSanitizer runtime not found (hipcc said {path!r}; "
+                           f"looked under {llvm})")
+    return path
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
-    print(path)
+    if "--print-asan-runtime" in sys.argv:
+        print(sanitizer_runtime())
+    else:
+        path = build(verbose="-v" in sys.argv, sanitize="--sanitize" in sys.argv)
+        print(path)

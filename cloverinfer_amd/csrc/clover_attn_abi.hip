@@ -555,8 +555,10 @@ int clv_paged_decode_fp8_partials(const clv_decode_args *a, const float *k_scale
   if (a == nullptr) return CLV_EINVAL;
   if (a->dtype != CLV_F16 && a->dtype != CLV_BF16) return CLV_EINVAL;
   if (a->head_dim != 128 || a->block_size < 16) return CLV_EUNSUPPORTED;
+  // The wave count sets the partial layout that clv_balanced_reduce reads,
+  // whose own default differs: it must be explicit here.
+  if (num_waves <= 0) return CLV_EINVAL;
   clv::DecodeParams p;
-  if (num_waves <= 0) num_waves = clv_default_num_waves_fp8();
   const int st = fill_balanced(a, num_waves, workspace, workspace_bytes, &p);
   if (st != CLV_OK || p.num_seqs == 0) return st;
   if (!k_scales || !v_scales) return CLV_EINVAL;

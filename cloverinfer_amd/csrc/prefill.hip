@@ -8,7 +8,9 @@
 // 0..i one at a time (append-then-attend).
 //
 // This file holds the VALU form (any dtype; one workgroup per query row and
-// kv head). The MFMA form for fp16/bf16 is in prefill_mfma.hip.
+// kv head). The MFMA form for fp16/bf16 is in prefill_mfma.hip. In both, a
+// row at index max_query_len or later of its chunk (a chunk longer than the
+// caller's max_query_len, a caller error) comes out as NaN.
 #include "attn_common.h"
 
 namespace clv {
@@ -38,6 +40,13 @@ __global__ void __launch_bounds__(NW * 64) chunked_prefill_valu(const PrefillPar
   const int g0 = (blockIdx.y - kvh * n_gchunks) * GM;
   const int ng = min(GM, p.group - g0);
   const int h0 = kvh * p.group + g0;
+  if (i >= p.max_query_len) {
+    const T nan = (T)__builtin_nanf("");
+    for (int idx = threadIdx.x; idx < ng * D; idx += NW * 64)
+      ((T *)p.out)[(int64_t)tok * p.out_stride_token +
+                   (int64_t)(h0 + idx / D) * p.out_stride_head + idx % D] = nan;
+    return;
+  }
 
   KvView kv;
   kv.bt = p.block_tables + (int64_t)s * p.max_blocks_per_seq;

@@ -522,7 +522,8 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       const int row = kWaveRows * wave + 16 * rt + 4 * j + e;
       const int tok = q0 + row / G;
       if (row >= bq * G || tok >= n_new) continue;
-      const float inv = l > 0.f ? 1.f / l : 0.f;
+      // A row at or past max_query_len (a caller error) is marked with NaN.
+      const float inv = tok >= p.max_query_len ? __builtin_nanf("") : l > 0.f ? 1.f / l : 0.f;
       // Lane n16 of MFMA m holds column d = 16m + n16.
       T *dst = (T *)p.out + (int64_t)(qs + tok) * p.out_stride_token +
                (int64_t)(kvh * G + row % G) * p.out_stride_head + n16;

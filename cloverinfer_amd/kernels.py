@@ -301,10 +301,13 @@ class AppendDecodeLaunch:
                              f"{tuple(value_new.shape)}")
         if key_new.dtype != k_cache.dtype or value_new.dtype != k_cache.dtype:
             raise ValueError("key_new/value_new dtype must match the cache dtype")
-        if key_new.stride() != value_new.stride() or key_new.stride(2) != 1:
-            key_new, value_new = key_new.contiguous(), value_new.contiguous()
+        key_new, value_new = self._rows(key_new, value_new)
         self.args = a
         self.num_waves = num_waves
+        # The launch holds the tensors whose addresses it passes (a contiguous
+        # copy made above would otherwise be freed, and its memory reused,
+        # before the kernel reads it); update() replaces them.
+        self._key_new, self._value_new = key_new, value_new
         self.key_ptr, self.value_ptr = key_new.data_ptr(), value_new.data_ptr()
         self.kv_new_strides = (key_new.stride(0), key_new.stride(1))
         lib = _native.load()
@@ -313,14 +316,32 @@ class AppendDecodeLaunch:
                                                                 num_waves)
         self._fn = lib.clv_paged_decode_append
 
+    @staticmethod
+    def _rows(key_new: torch.Tensor, value_new: torch.Tensor):
+        """The new rows as the kernel reads them: key and value with one
+        pair of (token, head) strides and a contiguous head_dim, copied to
+        contiguous tensors otherwise."""
+        if key_new.stride() != value_new.stride() or key_new.stride(2) != 1:
+            key_new, value_new = key_new.contiguous(), value_new.contiguous()
+        return key_new, value_new
+
     def update(self, out: torch.Tensor, q: torch.Tensor, block_tables: torch.Tensor,
                context_lens: torch.Tensor, max_context_len: int, key_new: torch.Tensor,
                value_new: torch.Tensor) -> None:
+        """Point the launch at this call's buffers. ``out``/``q``/tables must
+        have the shapes and strides of the build; new rows whose strides
+        differ from the build's are copied to contiguous tensors, and a launch
+        whose strides the copy still does not match raises ValueError."""
+        key_new, value_new = self._rows(key_new, value_new)
+        if (key_new.stride(0), key_new.stride(1)) != self.kv_new_strides:
+            raise ValueError(f"key_new/value_new strides {key_new.stride()} differ from the "
+                             f"launch's {self.kv_new_strides}")
         a = self.args
         a.out, a.q = out.data_ptr(), q.data_ptr()
         a.block_tables, a.max_blocks_per_seq = block_tables.data_ptr(), block_tables.shape[1]
         a.context_lens = context_lens.data_ptr()
         a.max_context_len = int(max_context_len)
+        self._key_new, self._value_new = key_new, value_new
         self.key_ptr, self.value_ptr = key_new.data_ptr(), value_new.data_ptr()
 
     def launch(self) -> None:
@@ -334,11 +355,17 @@ class AppendDecodeLaunch:
         """A callable that reissues this launch, as it stands now, on the
         current stream with no further Python work beyond the C call (for a
         caller that replays one step over fixed buffers); it returns the C
-        status code."""
+        status code. The callable holds a copy of the argument block and
+        the tensors it points into that the launch owns (the new rows if
+        they were copied, the workspace), so a later :meth:`update` or a
+        grown workspace does not change or free what it reads."""
         ws = splitk_workspace(self.device, self.workspace_bytes)
-        return functools.partial(self._fn, self.args, self.key_ptr, self.value_ptr,
+        a = type(self.args).from_buffer_copy(self.args)
+        call = functools.partial(self._fn, a, self.key_ptr, self.value_ptr,
                                  *self.kv_new_strides, self.num_waves, ws.data_ptr(), ws.numel(),
                                  _stream(self.device))
+        call.keepalive = (self._key_new, self._value_new, ws)
+        return call
 
 
 def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
@@ -482,8 +509,9 @@ def chunked_prefill(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
     its new tokens are the last ones of its ``context_lens[s]`` cached tokens,
     and row i sees positions ``<= context_lens[s] - n_s + i``.
     ``max_query_len`` must be at least every chunk length n_s (it sizes the
-    launch; rows past it come out as NaN); None computes it from
-    ``query_start_loc`` with one small device-to-host copy.
+    launch; a row i >= max_query_len of its chunk comes out as NaN, in every
+    kernel form); None computes it from ``query_start_loc`` with one small
+    device-to-host copy.
     """
     dev = _require_device(out, q, k_cache, v_cache, block_tables, context_lens, query_start_loc)
     _check_cache(k_cache, v_cache)

@@ -18,7 +18,10 @@ padding. Additive only:
   that ``get_kernel_inputs`` keeps for callers that want the tensors.
 
 Data movement and attention always run the HIP kernels through the C ABI;
-on a CPU device the bookkeeping works but the data path raises.
+on a CPU device the bookkeeping works but the data path raises. The
+reference's private slow path ``_paged_attention_ref``, against which its
+tests check the kernel, is plain torch on the device (an independent
+computation) and is never called by ``attention``.
 """
 from __future__ import annotations
 
@@ -228,10 +231,31 @@ class KVCacheManager:
         return self._decode(q, request_ids, partition_size)
 
     def _paged_attention_ref(self, q: torch.Tensor, request_ids: List[str]) -> torch.Tensor:
-        """The reference's second path for the same attention
-        (memory_manager.py:192-239, called by tests/verify_attention.py:124 to
-        check the kernel): here the single-pass HIP kernel, one workgroup per
-        (sequence, kv head) over the whole context, against which the default
-        schedule of ``attention`` can be compared. Same result contract as
-        ``attention``."""
-        return self._decode(q, request_ids, 0)
+        """The reference's second, slow path for the same attention
+        (memory_manager.py:192-239; tests/verify_attention.py:88-136 checks
+        the kernel against it), an independent computation in plain torch on
+        the pools' device: per request, gather its blocks, view them as
+        ``[n_blocks * block_size, num_kv_heads, head_dim][:context_len]``,
+        then ``softmax(q K^T * scale) V`` with query head h on kv head
+        ``h // (num_heads // num_kv_heads)``. The reference computes in q's
+        dtype; this computes in fp32 (never less accurate, and it keeps
+        torch's batched 16-bit products out) and returns q's dtype and device.
+        ``attention`` never takes this path, and like the data path it runs
+        on a HIP device only."""
+        self._require_gpu("_paged_attention_ref")
+        num_seqs, num_heads, head_dim = q.shape
+        hkv = self.num_kv_heads
+        g = num_heads // hkv
+        dev = self.k_cache.device
+        out = torch.empty_like(q)
+        for i, rid in enumerate(request_ids):
+            blocks = torch.tensor(self.block_tables[rid], dtype=torch.long, device=dev)
+            ctx = self.context_lens[rid]
+            k = self.k_cache[blocks].reshape(-1, hkv, head_dim)[:ctx].float()
+            v = self.v_cache[blocks].reshape(-1, hkv, head_dim)[:ctx].float()
+            qi = q[i].to(device=dev, dtype=torch.float32).reshape(hkv, g, head_dim)
+            scores = torch.matmul(qi, k.permute(1, 2, 0).contiguous()) * self.scale  # [Hkv, G, L]
+            weights = torch.softmax(scores, dim=-1)
+            ctx_out = torch.matmul(weights, v.permute(1, 0, 2).contiguous())  # [Hkv, G, D]
+            out[i] = ctx_out.reshape(num_heads, head_dim).to(device=q.device, dtype=q.dtype)
+        return out

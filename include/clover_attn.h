@@ -98,8 +98,8 @@ typedef struct clv_cache_args {
  * attends to cached positions p <= context_lens[s] - n_s + i (causal inside
  * the chunk, full view of everything cached before it).
  * max_query_len sizes the launch and must be >= every n_s (the host cannot
- * see query_start_loc, a device array): on the MFMA path, rows past it come
- * out as NaN.
+ * see query_start_loc, a device array): a row i >= max_query_len of its
+ * chunk comes out as NaN (every kernel form).
  */
 typedef struct clv_prefill_args {
   void *out;                      /* [num_tokens, num_heads, head_dim] */
@@ -289,9 +289,10 @@ int clv_paged_decode_fp8(const clv_decode_args *args, const float *k_scales,
 /*
  * First half of clv_paged_decode_fp8: the per-segment partials (normalised
  * context, row maximum, row sum) into the workspace, for clv_balanced_reduce
- * with the same arguments and the same explicit wave count to merge
- * (num_waves <= 0 means clv_default_num_waves_fp8() here but
- * clv_default_num_waves() in clv_balanced_reduce). For a caller that times the
+ * with the same arguments and the same wave count to merge. num_waves must
+ * be positive (CLV_EINVAL otherwise): the partial layout depends on it, and
+ * the defaults of this call and of clv_balanced_reduce differ
+ * (clv_default_num_waves_fp8() against clv_default_num_waves()). For a caller that times the
  * two kernels apart, or that merges partials from several GPUs of a
  * context-parallel decode. No counterpart in the reference.
  */

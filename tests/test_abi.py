@@ -120,3 +120,14 @@ def test_splitk_workspace_size(native_lib):
         _native.CLV_EINVAL  # partition not a multiple of 32
     assert native_lib.clv_paged_decode_splitk(ctypes.byref(a), 32, None, 0, None) == \
         _native.CLV_EWORKSPACE
+
+
+def test_fp8_partials_need_an_explicit_wave_count(native_lib):
+    """The partial layout depends on the wave count and the defaults of the
+    partials call and of clv_balanced_reduce differ: num_waves <= 0 is
+    refused before anything is launched."""
+    a = _valid_decode()
+    a.num_seqs = 1
+    for waves in (0, -1):
+        assert native_lib.clv_paged_decode_fp8_partials(
+            ctypes.byref(a), 0x3000, 0x3000, waves, None, 0, None) == _native.CLV_EINVAL

@@ -63,3 +63,18 @@ def test_default_bench_line_has_the_contract_fields():
         assert set(cpu) >= {"value", "unit", "cores", "kind", "sample"}, name
         assert cpu["kind"] == "port" and cpu["value"] > 0 and cpu["cores"] >= 1, name
         assert cpu["unit"] == e["unit"], name
+        # one timing rule: achieved = work per launch / back-to-back mean
+        assert roof["kernel_us"] == pytest.approx(
+            list(e["kernel_us_back_to_back"].values())[0]), name
+        scale = 1e9 if roof["unit"] == "GB/s" else 1e12
+        assert roof["achieved"] == pytest.approx(
+            roof["work_per_launch"] / (roof["kernel_us"] * 1e-6) / scale), name
+        # the timed launch's output against the oracle, every row
+        par = e["parity"]
+        assert par["within_bar"] and par["finite"], (name, par)
+        assert par["max_abs"] <= 2e-3 and par["max_rel"] <= 1e-2, (name, par)
+    assert r["parity"] == r["configs"]["qwen7b"]["parity"]
+    assert r["configs"]["qwen7b"]["parity"]["rows"] == 128
+    assert r["configs"]["llama7b"]["parity"]["rows"] == 64
+    assert r["configs"]["long32k"]["parity"]["rows"] == 16
+    assert r["configs"]["prefill"]["parity"]["rows"] == 8 * 512

@@ -107,3 +107,55 @@ def test_fused_append_out_of_range_positions(num_waves):
                                    num_waves=num_waves)
     torch.cuda.synchronize()
     assert _same_bits(kf.cpu(), k) and _same_bits(vf.cpu(), v)
+
+
+@pytest.mark.parametrize("long", [False, True], ids=["single-pass", "balanced"])
+def test_fused_append_strided_new_rows_and_reused_launch(long):
+    """New K/V rows given as transposed views (head-major storage) and with
+    different strides for key and value: the launch copies them to
+    contiguous rows and holds the copies until its kernels have read them.
+    The same launch, re-pointed with update() and replayed through bind(),
+    writes the next step's rows; pools and outputs equal the two-call form."""
+    hq, hkv, d, bs, dtype = 28, 4, 128, 16, torch.bfloat16
+    ctx0 = [40, 700 if long else 90, 17]
+    cap = [c + 2 for c in ctx0]
+    k, v, tables = make_paged_kv(91, cap, hkv, d, bs, dtype, spare_blocks=2)
+    kf, vf = k.to(DEV), v.to(DEV)
+    ku, vu = k.clone().to(DEV), v.clone().to(DEV)
+    bt = padded_tables(tables).to(DEV)
+    g = torch.Generator().manual_seed(92)
+    scale = d ** -0.5
+    launch = None
+    for step in range(2):
+        lens_h = [c + step for c in ctx0]
+        lens = torch.tensor(lens_h, dtype=torch.int32, device=DEV)
+        q = torch.randn(3, hq, d, generator=g).to(dtype).to(DEV)
+        # key: [hkv, S, d] storage seen as [S, hkv, d]; value contiguous
+        kn = torch.randn(hkv, 3, d, generator=g).to(dtype).to(DEV).transpose(0, 1)
+        vn = torch.randn(3, hkv, d, generator=g).to(dtype).to(DEV)
+        assert kn.stride() != vn.stride()
+        out_f = torch.empty_like(q)
+        if launch is None:
+            launch = kernels.AppendDecodeLaunch(out_f, q, kf, vf, bt, lens, bs, max(lens_h), kn,
+                                                vn, scale=scale)
+            launch.launch()
+        else:
+            launch.update(out_f, q, bt, lens, max(lens_h), kn, vn)
+            call = launch.bind()
+            del kn, vn  # the launch holds the contiguous copies it reads
+            junk = torch.full((64, hkv, d), float("nan"), dtype=dtype, device=DEV)
+            kernels._native.check(call(), "clv_paged_decode_append")
+            del junk
+        slots = [t[(c - 1) // bs] * bs + (c - 1) % bs for t, c in zip(tables, lens_h)]
+        knc = launch._key_new
+        vnc = launch._value_new
+        kernels.reshape_and_cache(knc, vnc, ku, vu,
+                                  torch.tensor(slots, dtype=torch.int64, device=DEV))
+        out_u = torch.empty_like(q)
+        kernels.paged_attention(out_u, q, ku, vu, bt, lens, bs, max(lens_h), scale=scale,
+                                **_fused_schedule(hq, hkv, max(lens_h)))
+        torch.cuda.synchronize()
+        assert _same_bits(kf, ku) and _same_bits(vf, vu), f"pools differ at step {step}"
+        assert torch.equal(out_f, out_u), f"step {step}"
+        ref = oa.paged_decode(q.cpu(), ku.cpu(), vu.cpu(), tables, lens_h, scale)
+        assert_attention_close(out_f.cpu(), ref, what=f"strided rows, step {step}")

@@ -182,8 +182,9 @@ def test_reference_kat_identical_rows_on_gpu():
 
 def test_reference_check_kernel_vs_reference_flow():
     """tests/verify_attention.py:88-136 as the reference runs it against the
-    drop-in: attention() (the default schedule) and _paged_attention_ref()
-    (the single-pass kernel) agree to allclose(atol=1e-2, rtol=1e-2), both
+    drop-in: attention() (the kernel) and _paged_attention_ref() (an
+    independent plain-torch gather + softmax) agree to allclose(atol=1e-2,
+    rtol=1e-2), both
     return tensors like q, and both equal the oracle. A query in another dtype
     than the pool comes back in its own dtype."""
     m = KVCacheManager(100, 16, 4, 32, dtype=torch.float16, device=DEV)
@@ -201,11 +202,36 @@ def test_reference_check_kernel_vs_reference_flow():
         assert o.shape == q.shape and o.dtype == q.dtype and o.device == q.device
     assert torch.allclose(out_kernel, out_ref, atol=1e-2, rtol=1e-2)
     ref = oa.attend(q[0].cpu(), k.cpu().expand(50, 4, 32), v.cpu().expand(50, 4, 32), 32 ** -0.5)
-    assert_attention_close(out_ref[0], ref, what="single pass")
+    assert_attention_close(out_ref[0], ref, what="plain-torch reference path")
+    assert_attention_close(out_kernel[0], ref, what="kernel")
     q32 = q.float()
     o32 = m.attention(q32, ["req_test_kernel"])
     assert o32.dtype == torch.float32 and o32.device == q32.device
     assert_attention_close(o32[0], ref, what="fp32 query over an fp16 pool")
+
+
+def test_paged_attention_ref_is_independent_and_gqa():
+    """_paged_attention_ref (plain torch gather + softmax, the reference's
+    memory_manager.py:192-239 with the repeat_kv grouping) equals the oracle
+    on a GQA pool with ragged contexts spanning several blocks, as does
+    attention() over the same requests."""
+    m = KVCacheManager(64, 16, 28, 128, dtype=torch.bfloat16, device=DEV, num_kv_heads=4)
+    g = torch.Generator().manual_seed(21)
+    rids, kv = ["a", "b", "c"], {}
+    for rid, n in zip(rids, (1, 37, 300)):
+        kd = torch.randn(n, 4, 128, generator=g).to(torch.bfloat16)
+        vd = torch.randn(n, 4, 128, generator=g).to(torch.bfloat16)
+        kv[rid] = (kd, vd)
+        m.load_initial_kv(rid, kd.to(DEV), vd.to(DEV))
+    q = torch.randn(3, 28, 128, generator=g).to(torch.bfloat16)
+    ref = torch.stack([oa.attend(q[i], kv[r][0], kv[r][1], 128 ** -0.5)
+                       for i, r in enumerate(rids)])
+    out_ref = m._paged_attention_ref(q.to(DEV), rids)
+    out = m.attention(q.to(DEV), rids)
+    torch.cuda.synchronize()
+    assert out_ref.dtype == torch.bfloat16
+    assert_attention_close(out_ref.cpu(), ref, what="_paged_attention_ref, GQA")
+    assert_attention_close(out.cpu(), ref, what="attention, GQA")
 
 
 # ---------------------------------------------------------------- configs

@@ -148,18 +148,19 @@ def test_prefill_bf16_values_beyond_fp16_range():
     assert_attention_close(got, ref, what="prefill bf16 beyond fp16 range")
 
 
-def test_prefill_max_query_len_none_and_too_small():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])  # MFMA and VALU kernels
+def test_prefill_max_query_len_none_and_too_small(dtype):
     """max_query_len=None is computed from query_start_loc; a value below the
-    longest chunk leaves that chunk's rows past it as NaN on the MFMA path
-    (a loud error, not stale memory), and the rows it covers stay exact."""
+    longest chunk makes that chunk's rows at or past it NaN (a loud error, not
+    stale memory), and the other rows stay exact, in both kernel forms."""
     cached, new = [30, 200], [300, 40]
-    q, k, v, tables, ctx, qsl = build(77, cached, new, 16, 4, 128, 16, torch.bfloat16)
+    q, k, v, tables, ctx, qsl = build(77, cached, new, 16, 4, 128, 16, dtype)
     scale = 1.0 / math.sqrt(128)
     ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
     kg, vg, bt = k.to(DEV), v.to(DEV), padded_tables(tables).to(DEV)
     cl = torch.tensor(ctx, dtype=torch.int32, device=DEV)
     qs = torch.tensor(qsl, dtype=torch.int32, device=DEV)
-    out = torch.full((q.shape[0], 16, 128), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = torch.full((q.shape[0], 16, 128), 7.0, dtype=dtype, device=DEV)
     kernels.chunked_prefill(out, q.to(DEV), kg, vg, bt, cl, qs, None, scale=scale)
     torch.cuda.synchronize()
     assert_attention_close(out.cpu(), ref, what="max_query_len=None")
@@ -167,7 +168,6 @@ def test_prefill_max_query_len_none_and_too_small():
     kernels.chunked_prefill(out, q.to(DEV), kg, vg, bt, cl, qs, 40, scale=scale)
     torch.cuda.synchronize()
     got = out.cpu().float()
-    covered = 64  # one query tile: 256 rows / 4 query heads per kv head
-    assert_attention_close(got[:covered], ref[:covered], what="rows inside the grid")
-    assert torch.isnan(got[covered:300]).all(), "rows past the grid must come out as NaN"
+    assert_attention_close(got[:40], ref[:40], what="rows below max_query_len")
+    assert torch.isnan(got[40:300]).all(), "rows at or past max_query_len must come out as NaN"
     assert_attention_close(got[300:], ref[300:], what="the second, shorter chunk")

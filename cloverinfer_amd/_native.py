@@ -211,6 +211,37 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_host = None
+_host_tried = False
+
+
+def load_host():
+    """The node backend's native payload gather (cloverinfer_amd/_lib/_clv_host.so,
+    built by cloverinfer_amd/build.py), or None when it is absent or does not
+    load: it is host plumbing, and the backend then stages payloads with
+    torch.stack."""
+    global _host, _host_tried
+    if _host_tried:
+        return _host
+    with _lock:
+        if not _host_tried:
+            import importlib.util
+
+            import torch  # noqa: F401  (its libraries resolve the module's)
+
+            path = _build.HOST_EXT_PATH
+            if os.path.exists(path):
+                try:
+                    spec = importlib.util.spec_from_file_location(_build.HOST_EXT_NAME, path)
+                    mod = importlib.util.module_from_spec(spec)
+                    spec.loader.exec_module(mod)
+                    _host = mod
+                except ImportError:
+                    _host = None
+            _host_tried = True
+    return _host
+
+
 def status_string(code: int) -> str:
     return load().clv_status_string(code).decode()
 

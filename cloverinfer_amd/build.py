@@ -46,6 +46,12 @@ SOURCES = [
 
 ARCH = "gfx950"
 
+# The node backend's native payload gather (a Python extension on torch's C++
+# API, host code only; cloverinfer_amd/host/node_gather.cpp).
+HOST_EXT_NAME = "_clv_host"
+HOST_EXT_SRC = os.path.join(PKG_DIR, "host", "node_gather.cpp")
+HOST_EXT_PATH = os.path.join(LIB_DIR, HOST_EXT_NAME + ".so")
+
 SANITIZE_LIB_PATH = os.path.join(LIB_DIR, "sanitize", LIB_NAME)
 # Host-only sanitizer flags: each one behind -Xarch_host, so that the gfx950
 # device code is compiled exactly as in the normal build.
@@ -125,6 +131,33 @@ def build(verbose: bool = False, jobs: int | None = None, sanitize: bool = False
     return lib_path
 
 
+def build_host_ext(verbose: bool = False) -> str:
+    """Compile the node backend's payload gather (g++, against the installed
+    torch) into HOST_EXT_PATH; returns its path."""
+    import sysconfig
+
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    os.makedirs(LIB_DIR, exist_ok=True)
+    inc = [f for p in ce.include_paths() for f in ("-I", p)]
+    inc += ["-I", sysconfig.get_paths()["include"]]
+    lib = ce.library_paths()[0]
+    tmp = HOST_EXT_PATH + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", *inc,
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           f"-DTORCH_EXTENSION_NAME={HOST_EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           HOST_EXT_SRC, "-o", tmp, f"-L{lib}", "-lc10", "-ltorch", "-ltorch_cpu",
+           "-ltorch_python", f"-Wl,-rpath,{lib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for {HOST_EXT_SRC}:\n{res.stderr[-4000:]}")
+    os.replace(tmp, HOST_EXT_PATH)
+    return HOST_EXT_PATH
+
+
 def sanitizer_runtime() -> str:
     """Path of the AddressSanitizer runtime (which carries the
     UndefinedBehaviorSanitizer checks too) that a process loading the
@@ -143,5 +176,8 @@ if __name__ == "__main__":
     if "--print-asan-runtime" in sys.argv:
         print(sanitizer_runtime())
     else:
-        path = build(verbose="-v" in sys.argv, sanitize="--sanitize" in sys.argv)
+        sanitize = "--sanitize" in sys.argv
+        path = build(verbose="-v" in sys.argv, sanitize=sanitize)
         print(path)
+        if not sanitize:
+            print(build_host_ext(verbose="-v" in sys.argv))

@@ -590,7 +590,7 @@ class GpuAttentionBackend:
             launch = self._launches.get(lkey) if self.partition_size is None else None
             if launch is not None:
                 launch.update(ctx_out, q, bt, ctx_dev, max_len, k, v)
-                launch.launch()
+                launch.launch(stream.cuda_stream)
             else:
                 kp, vp = self.k_pools[layer], self.v_pools[layer]
                 if self.partition_size is None and kernels.append_fusable(q, kp, n):
@@ -599,7 +599,7 @@ class GpuAttentionBackend:
                     launch = kernels.AppendDecodeLaunch(ctx_out, q, kp, vp, bt, ctx_dev, bs,
                                                         max_len, k, v, scale=score_scale)
                     self._launches[lkey] = launch
-                    launch.launch()
+                    launch.launch(stream.cuda_stream)
                 else:
                     self._append(k, v, layer, slots_dev)
                     kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
@@ -632,7 +632,7 @@ class GpuAttentionBackend:
                                          non_blocking=True)
                 # The per-item views are built while the GPU works.
                 out = res if packed else list(res.unbind(0))
-                torch.cuda.current_stream(self.device).synchronize()
+                stream.synchronize()
                 return out
             res = ctx_out.to(device=qdev, dtype=qdt).view(n, 1, hq, d)
             return res if packed else list(res.unbind(0))

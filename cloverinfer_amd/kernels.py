@@ -113,12 +113,13 @@ def choose_partition(num_seqs: int, num_kv_heads: int, group: int, max_context_l
     return DEFAULT_PARTITION
 
 
-def splitk_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+def splitk_workspace(dev: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """A cached, grow-only uint8 workspace of at least ``nbytes`` for the
     current stream of ``dev`` (one per stream, so that launches on different
-    streams never share partials)."""
+    streams never share partials); ``stream``: that stream's handle, when the
+    caller has looked it up already."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (idx, _stream(torch.device("cuda", idx)))
+    key = (idx, stream if stream is not None else _stream(torch.device("cuda", idx)))
     with _ws_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
@@ -344,11 +345,14 @@ class AppendDecodeLaunch:
         self._key_new, self._value_new = key_new, value_new
         self.key_ptr, self.value_ptr = key_new.data_ptr(), value_new.data_ptr()
 
-    def launch(self) -> None:
-        """Issue on the current stream (with that stream's workspace)."""
-        ws = splitk_workspace(self.device, self.workspace_bytes)
+    def launch(self, stream: int | None = None) -> None:
+        """Issue on the current stream (with that stream's workspace);
+        ``stream``: the current stream's handle, when the caller has it."""
+        if stream is None:
+            stream = _stream(self.device)
+        ws = splitk_workspace(self.device, self.workspace_bytes, stream)
         _native.check(self._fn(self.args, self.key_ptr, self.value_ptr, *self.kv_new_strides,
-                               self.num_waves, ws.data_ptr(), ws.numel(), _stream(self.device)),
+                               self.num_waves, ws.data_ptr(), ws.numel(), stream),
                       "clv_paged_decode_append")
 
     def bind(self):

@@ -155,6 +155,11 @@ SIGNATURES = {
         [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, ctypes.c_int64, ctypes.c_int64, _c_i32,
          _c_ptr, ctypes.c_size_t, _c_ptr],
     ),
+    "clv_balanced_reduce_append": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeArgs), _c_ptr, _c_ptr, ctypes.c_int64, ctypes.c_int64, _c_ptr,
+         _c_i32, _c_ptr, ctypes.c_size_t, _c_ptr],
+    ),
     "clv_reshape_and_cache_fp8": (
         ctypes.c_int, [ctypes.POINTER(CacheArgs), _c_ptr, _c_ptr, _c_ptr],
     ),
@@ -240,6 +245,32 @@ def load_host():
                     _host = None
             _host_tried = True
     return _host
+
+
+_host_ptr_fns = None
+
+
+def mapped_device_address(host_ptr: int) -> int | None:
+    """The device address of pinned host memory that kernels can access
+    directly (hipHostGetDevicePointer), or None when the memory is not
+    mapped for the device. Resolved through the library's own HIP runtime
+    (dlsym on its handle searches its dependencies), the one torch uses. A
+    refused query's error is cleared, so that the next launch's error check
+    does not report it."""
+    global _host_ptr_fns
+    if _host_ptr_fns is None:
+        lib = load()
+        fn, last = lib.hipHostGetDevicePointer, lib.hipGetLastError
+        fn.restype = last.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
+        last.argtypes = []
+        _host_ptr_fns = (fn, last)
+    fn, last = _host_ptr_fns
+    dev = ctypes.c_void_p()
+    if fn(ctypes.byref(dev), ctypes.c_void_p(host_ptr), 0) != 0:
+        last()
+        return None
+    return dev.value or None
 
 
 def status_string(code: int) -> str:

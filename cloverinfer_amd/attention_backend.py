@@ -45,6 +45,10 @@ class _Request:
 _get_layer = operator.itemgetter("layer_idx")
 _get_rid = operator.itemgetter("request_id")
 _get_row = operator.attrgetter("row")
+_get_scale = operator.methodcaller("get", "score_scale", 1.0)
+_get_query = operator.itemgetter("query")
+_get_key = operator.itemgetter("key")
+_get_value = operator.itemgetter("value")
 
 
 def _align(n: int) -> int:
@@ -102,6 +106,7 @@ class GpuAttentionBackend:
         self.k_scales: Optional[torch.Tensor] = None  # fp8 pools: [num_kv_heads] on the device
         self.v_scales: Optional[torch.Tensor] = None
         self.k_pools: Optional[torch.Tensor] = None  # [L, NB, bs, Hkv, D]
+        self._layer_pools: List[tuple] = []  # (k, v) views of each layer's pools
         self.v_pools: Optional[torch.Tensor] = None
         self.num_layers = 0
         self.free_blocks: List[int] = list(range(num_blocks))
@@ -116,6 +121,8 @@ class GpuAttentionBackend:
         self._htab = np.zeros((0, 0), dtype=np.int64)
         self._bshift = block_size.bit_length() - 1
         self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
+        self._stage_np: Dict[str, np.ndarray] = {}  # their bytes as numpy arrays
+        self._split_ok: Dict[tuple, bool] = {}  # batch shapes the split decode covers
         self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
         # Device twin of the staging buffer, reused by every wave: a wave
         # whose results stay on the device returns while its kernels may still
@@ -128,6 +135,13 @@ class GpuAttentionBackend:
         self._dstage_free: Optional[torch.cuda.Event] = None  # after the last reader of _dstage
         self._dstage_stream: Optional[int] = None  # stream of that reader
         self._dout: Optional[torch.Tensor] = None
+        # The split decode's second upload (k, v, slots, table updates) goes
+        # on a copy stream of its own (default priority), so that it runs
+        # while the decode over the cached tokens does; events order it after
+        # the first upload and before the merge.
+        self._up_stream: Optional[torch.cuda.Stream] = None
+        self._up_done: Optional[torch.cuda.Event] = None
+        self._h1_done: Optional[torch.cuda.Event] = None
         self._launches: Dict[tuple, "kernels.AppendDecodeLaunch"] = {}
         self._views: Dict[tuple, tuple] = {}  # device views into _dstage per batch shape
         self._filled_host = False
@@ -154,6 +168,7 @@ class GpuAttentionBackend:
         self.k_pools = torch.zeros(shape, dtype=dtype, device=self.device)
         self.v_pools = torch.zeros(shape, dtype=dtype, device=self.device)
         self.num_layers = num_layers
+        self._layer_pools = [(self.k_pools[i], self.v_pools[i]) for i in range(num_layers)]
 
     @property
     def _fp8(self) -> bool:
@@ -339,7 +354,7 @@ class GpuAttentionBackend:
             # The node's batch: one layer and scale, distinct known requests,
             # checked with a few C-level passes instead of a loop per item.
             layers = set(map(_get_layer, items))
-            scales = {it.get("score_scale", 1.0) for it in items}
+            scales = set(map(_get_scale, items))
             if len(layers) == 1 and len(scales) == 1:
                 reqs = list(map(requests.get, map(_get_rid, items)))
                 if None not in reqs and len(set(map(_get_row, reqs))) == len(reqs):
@@ -371,8 +386,8 @@ class GpuAttentionBackend:
 
     @staticmethod
     def _payloads(items: List[Dict[str, object]]):
-        return ([it["query"] for it in items], [it["key"] for it in items],
-                [it["value"] for it in items])
+        return (list(map(_get_query, items)), list(map(_get_key, items)),
+                list(map(_get_value, items)))
 
     def decode_layer_packed(self, request_ids: List[str], layer_idx: int, query: torch.Tensor,
                             key: torch.Tensor, value: torch.Tensor,
@@ -411,6 +426,8 @@ class GpuAttentionBackend:
         if buf is None or buf.dtype != dtype or buf.numel() < n:
             buf = torch.empty(max(n, 1), dtype=dtype, pin_memory=True)
             self._stage[name] = buf
+            self._stage_np[name] = buf.numpy()
+            self._views.clear()  # they hold slices of the old buffer
         return buf[:n].view(*shape)
 
     def _fill(self, ts: List[torch.Tensor], heads: int, d: int, dt: torch.dtype,
@@ -489,88 +506,82 @@ class GpuAttentionBackend:
         dt = self._compute_dtype(q0.dtype)
         kdt = self._append_dtype(ks[0].dtype)  # fp8 pools: quantised once, from the payload
 
-        # One pinned buffer, one upload: q | k | v | int32 context lengths and
-        # rows | int64 slots | table updates (int64 flat table indices, then
-        # int32 blocks). The updates come last: their count is known only
-        # after the bookkeeping, and a wave takes at most one new block per
-        # request. Everything before them sits at offsets fixed by the batch
-        # shape, so their device views are built once per shape.
+        # One pinned buffer for the call's uploads: q | int32 context lengths
+        # and rows | k | v | int64 slots | table updates (int64 flat table
+        # indices, then int32 blocks). The updates come last: their count is
+        # known only after the bookkeeping, and a wave takes at most one new
+        # block per request. Everything before them sits at offsets fixed by
+        # the batch shape, so their device views are built once per shape.
+        # q and the lengths lead, so that the split decode below can upload
+        # them and start before k, v and the bookkeeping are done.
         qb = n * hq * d * torch.finfo(dt).bits // 8
         kb = n * hkv * d * torch.finfo(kdt).bits // 8
-        o_k = _align(qb)
+        o_i = _align(qb)
+        o_k = o_i + _align(8 * n)
         o_v = o_k + _align(kb)
-        o_i = o_v + _align(kb)
-        o_w = o_i + _align(8 * n)
+        o_w = o_v + _align(kb)
         o_u = o_w + 8 * n
         nu_max = self.tables.pending_count() + n
         buf = self._staging("wave", (o_u + 12 * nu_max,), torch.uint8)
+        bnp = self._stage_np["wave"]
         self._filled_host = self._gathered = False
         q = self._fill(qs, hq, d, dt, buf[:qb])
         q_host = self._filled_host
         q_same = self._gathered and dt == q0.dtype  # every query: a host tensor of q0's dtype
-        k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
-        v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
 
-        # Bookkeeping over the requests' rows: the new token of request i
-        # goes to position pos[i] of this layer (a request whose blocks are
-        # full takes one more first).
+        # Position of each request's new token in this layer: its cached
+        # length (a request whose blocks are full takes one more first).
         rows = np.fromiter(map(_get_row, reqs), dtype=np.int64, count=n)
         pos = self._lens[rows, layer]
-        full = np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist()
-        if len(full) > len(self.free_blocks):
-            raise RuntimeError("OOM during append")
-        for i in full:
-            self._grow_request(reqs[i])
-        slots = self._htab[rows, pos >> self._bshift] * bs + (pos & (bs - 1))
-        lens = pos + 1
-        self._lens[rows, layer] = lens
-        upd = self.tables.take_pending()
-        nu = len(upd)
+        narrow = bnp[o_i:o_i + 8 * n].view(np.int32)
+        narrow[n:] = rows
+        max_old = int(pos.max())
+        kp, vp = self._layer_pools[layer]
+        # The split decode (partials over the cached tokens now, the new token
+        # merged in by the reduce later) lets the GPU attend while the host
+        # stages k and v and does the bookkeeping. Short contexts keep the
+        # single-pass fused launch, fp8 pools and a forced split-K their own.
+        skey = (n, hq)
+        split_ok = self._split_ok.get(skey)
+        if split_ok is None:
+            split_ok = self._split_ok[skey] = (not self._fp8 and
+                                               kernels.append_fusable_shape(hq, kp, n))
+        split = split_ok and self.partition_size is None and max_old + 1 > 512
+        stream = torch.cuda.current_stream(self.device)
+        upd: list = []
         applied = False
+        issued = False  # a kernel that reads the device staging is queued
+        h1 = False  # the split decode's first upload is issued, its second not
+        direct = None  # the pinned result tensor the merge writes, if any
         try:
-            total = o_u + 12 * nu
-            narrow = buf[o_i:o_i + 8 * n].numpy().view(np.int32)
-            narrow[:n] = lens
-            narrow[n:] = rows
-            buf[o_w:o_u].numpy().view(np.int64)[:] = slots
-            if nu:
-                flat, blocks = self.tables.flat_updates(upd)
-                buf[o_u:o_u + 8 * nu].numpy().view(np.int64)[:] = flat
-                buf[o_u + 8 * nu:total].numpy().view(np.int32)[:] = blocks
-            stream = torch.cuda.current_stream(self.device)
             if self._dstage_free is not None and self._dstage_stream != stream.cuda_stream:
                 stream.wait_event(self._dstage_free)  # the previous wave's kernels read it
-            if self._dstage is None or self._dstage.numel() < total:
-                self._dstage = torch.empty(max(2 * total, 1 << 20), dtype=torch.uint8,
+            total_max = o_u + 12 * nu_max
+            if self._dstage is None or self._dstage.numel() < total_max:
+                self._dstage = torch.empty(max(2 * total_max, 1 << 20), dtype=torch.uint8,
                                            device=self.device)
                 self._views.clear()
-            dev = self._dstage[:total]
-            dev.copy_(buf[:total], non_blocking=True)
             if self._stage_done is None:
                 self._stage_done = torch.cuda.Event()
-            self._stage_done.record(stream)
             vkey = (n, hq, hkv, d, dt, kdt)
             views = self._views.get(vkey)
             if views is None:
                 narrow_dev = self._dstage[o_i:o_i + 8 * n].view(torch.int32)
+                hb = self._stage["wave"]
+                e = o_u + 12 * n  # end of the uploads with up to n table updates
                 views = (self._dstage[:qb].view(dt).view(n, hq, d),
                          self._dstage[o_k:o_k + kb].view(kdt).view(n, hkv, d),
                          self._dstage[o_v:o_v + kb].view(kdt).view(n, hkv, d),
                          narrow_dev[:n], narrow_dev[n:],
-                         self._dstage[o_w:o_u].view(torch.int64))
+                         self._dstage[o_w:o_u].view(torch.int64),
+                         # (device, host) byte ranges of the uploads: q and
+                         # the integers, the integers alone, the rest, all
+                         (self._dstage[:o_k], hb[:o_k]), (self._dstage[o_i:o_k], hb[o_i:o_k]),
+                         (self._dstage[o_k:e], hb[o_k:e]), (self._dstage[:e], hb[:e]))
                 self._views[vkey] = views
-            q = views[0] if q is None else q
-            k = views[1] if k is None else k
-            v = views[2] if v is None else v
+            q_staged = q is None  # the queries are in the pinned buffer
+            q = views[0] if q_staged else q
             ctx_dev, rows_dev, slots_dev = views[3], views[4], views[5]
-            if nu:
-                self.tables.apply_flat(dev[o_u:o_u + 8 * nu].view(torch.int64),
-                                       dev[o_u + 8 * nu:total].view(torch.int32))
-            applied = True
-            if rows[-1] - rows[0] == n - 1 and (n < 3 or bool((np.diff(rows) == 1).all())):
-                bt = self.tables.rows_range(int(rows[0]), n)
-            else:
-                bt = self.tables.rows(rows.tolist(), rows_dev)
             to_host = (not qs.is_cuda) if packed else (q_host or all(not t.is_cuda for t in qs))
             if to_host:
                 # The call waits for its results: the output buffer is free
@@ -581,39 +592,139 @@ class GpuAttentionBackend:
                 ctx_out = self._dout[:q.numel()].view(q.shape)
             else:
                 ctx_out = torch.empty_like(q)
-            max_len = int(lens.max())
-            # Append and decode in one call (the new rows land at position
-            # lens - 1, the slots computed above) where the fused kernel covers
-            # the shape; the launch is built once per batch shape, layer and
-            # scale (the pools are never reallocated).
-            lkey = (n, hq, layer, float(score_scale), dt, kdt, q.stride(), k.stride())
-            launch = self._launches.get(lkey) if self.partition_size is None else None
-            if launch is not None:
-                launch.update(ctx_out, q, bt, ctx_dev, max_len, k, v)
-                launch.launch(stream.cuda_stream)
+
+            def table():
+                if rows[-1] - rows[0] == n - 1 and (n < 3 or bool((np.diff(rows) == 1).all())):
+                    return self.tables.rows_range(int(rows[0]), n)
+                return self.tables.rows(rows.tolist(), rows_dev)
+
+            launch = None
+            if split:
+                # Upload q, the cached lengths and the rows; attend over the
+                # cached tokens.
+                narrow[:n] = pos
+                dst, src = views[6] if q_staged else views[7]
+                dst.copy_(src, non_blocking=True)
+                h1 = True
+                if self._h1_done is None:
+                    self._h1_done = torch.cuda.Event()
+                    self._up_done = torch.cuda.Event()
+                    self._up_stream = torch.cuda.Stream(device=self.device)
+                self._h1_done.record(stream)
+                bt = table()
+                lkey = ("split", n, hq, layer, float(score_scale), dt, q.stride())
+                launch = self._launches.get(lkey)
+                if launch is None:
+                    if len(self._launches) >= 256:
+                        self._launches.clear()
+                    launch = kernels.SplitAppendDecode(ctx_out, q, kp, vp, bt, ctx_dev, bs,
+                                                       max_old, scale=score_scale)
+                    self._launches[lkey] = launch
+                else:
+                    launch.update(ctx_out, q, bt, ctx_dev, max_old)
+                launch.partials(stream.cuda_stream)
+                issued = True
+
+            k = self._fill(ks, hkv, d, kdt, buf[o_k:o_k + kb])
+            v = self._fill(vs, hkv, d, kdt, buf[o_v:o_v + kb])
+            full = np.nonzero(pos >= (self._nblk[rows] << self._bshift))[0].tolist()
+            if len(full) > len(self.free_blocks):
+                raise RuntimeError("OOM during append")
+            for i in full:
+                self._grow_request(reqs[i])
+            slots = self._htab[rows, pos >> self._bshift] * bs + (pos & (bs - 1))
+            lens = pos + 1
+            self._lens[rows, layer] = lens
+            upd = self.tables.take_pending()
+            nu = len(upd)
+            total = o_u + 12 * nu
+            bnp[o_w:o_u].view(np.int64)[:] = slots
+            if nu:
+                flat, blocks = self.tables.flat_updates(upd)
+                bnp[o_u:o_u + 8 * nu].view(np.int64)[:] = flat
+                bnp[o_u + 8 * nu:total].view(np.int32)[:] = blocks
+            k = views[1] if k is None else k
+            v = views[2] if v is None else v
+            if split:
+                # The rest (k, v, slots and table updates) on the copy stream,
+                # after the first upload and after the kernels of the previous
+                # wave that read the device staging; then merge the new tokens
+                # in (the reduce also writes their rows at the slots).
+                up = self._up_stream
+                up.wait_event(self._h1_done)
+                if self._dstage_free is not None:
+                    up.wait_event(self._dstage_free)
+                dst, src = views[8] if nu <= n else (self._dstage[o_k:total], buf[o_k:total])
+                with torch.cuda.stream(up):
+                    dst.copy_(src, non_blocking=True)
+                self._up_done.record(up)
+                self._stage_done.record(up)  # both uploads (up waited for the first)
+                h1 = False
+                stream.wait_event(self._up_done)
+                if nu:
+                    self.tables.apply_flat(self._dstage[o_u:o_u + 8 * nu].view(torch.int64),
+                                           self._dstage[o_u + 8 * nu:total].view(torch.int32))
+                applied = True
+                # Results that go to the host in the queries' dtype are
+                # written by the merge straight into the pinned tensor the
+                # call returns, where the device can address it: no copy back.
+                if to_host and dt == q0.dtype and q0.device.type == "cpu" and (packed or q_same):
+                    direct = torch.empty((n, 1, hq, d), dtype=dt, pin_memory=True)
+                    addr = _native.mapped_device_address(direct.data_ptr())
+                    if addr is None:
+                        direct = None
+                launch.reduce(k, v, slots_dev, stream.cuda_stream,
+                              out_address=addr if direct is not None else None)
             else:
-                kp, vp = self.k_pools[layer], self.v_pools[layer]
-                if self.partition_size is None and kernels.append_fusable(q, kp, n):
+                narrow[:n] = lens
+                dst, src = views[9] if nu <= n else (self._dstage[:total], buf[:total])
+                dst.copy_(src, non_blocking=True)
+                self._stage_done.record(stream)
+                if nu:
+                    self.tables.apply_flat(self._dstage[o_u:o_u + 8 * nu].view(torch.int64),
+                                           self._dstage[o_u + 8 * nu:total].view(torch.int32))
+                applied = True
+                bt = table()
+                max_len = int(lens.max())
+                # Append and decode in one call (the new rows land at
+                # position lens - 1, the slots computed above) where the
+                # fused kernel covers the shape; the launch is built once per
+                # batch shape, layer and scale (the pools are never
+                # reallocated).
+                lkey = (n, hq, layer, float(score_scale), dt, kdt, q.stride(), k.stride())
+                launch = self._launches.get(lkey) if self.partition_size is None else None
+                if launch is not None:
+                    launch.update(ctx_out, q, bt, ctx_dev, max_len, k, v)
+                    issued = True
+                    launch.launch(stream.cuda_stream)
+                elif self.partition_size is None and kernels.append_fusable(q, kp, n):
                     if len(self._launches) >= 256:
                         self._launches.clear()
                     launch = kernels.AppendDecodeLaunch(ctx_out, q, kp, vp, bt, ctx_dev, bs,
                                                         max_len, k, v, scale=score_scale)
                     self._launches[lkey] = launch
+                    issued = True
                     launch.launch(stream.cuda_stream)
                 else:
+                    issued = True
                     self._append(k, v, layer, slots_dev)
                     kernels.paged_attention(ctx_out, q, kp, vp, bt, ctx_dev, bs, max_len,
-                                            scale=score_scale, partition_size=self.partition_size,
+                                            scale=score_scale,
+                                            partition_size=self.partition_size,
                                             k_scale=self.k_scales, v_scale=self.v_scales)
         except BaseException:
             self._lens[rows, layer] = pos
             if not applied:
                 self.tables.requeue(upd)
+            if h1:  # the pinned buffer is read until the first upload is done
+                self._stage_done.record(stream)
             raise
-        if self._dstage_free is None:
-            self._dstage_free = torch.cuda.Event()
-        self._dstage_free.record(stream)
-        self._dstage_stream = stream.cuda_stream
+        finally:
+            if issued:
+                if self._dstage_free is None:
+                    self._dstage_free = torch.cuda.Event()
+                self._dstage_free.record(stream)
+                self._dstage_stream = stream.cuda_stream
         if layer == self.num_layers - 1:
             self._ctx[rows] += 1
         self.stats["decode_items"] += n
@@ -621,6 +732,10 @@ class GpuAttentionBackend:
         # Outputs in each query's dtype and on its device: one copy for the
         # batch when the queries agree (the node's case), per item otherwise.
         qdt, qdev = q0.dtype, q0.device
+        if direct is not None:
+            out = direct if packed else list(direct.unbind(0))
+            stream.synchronize()
+            return out
         if packed or q_same or (all(t.dtype == qdt for t in qs) and (
                 (qdev.type == "cpu" and to_host) or all(t.device == qdev for t in qs))):
             if qdev.type == "cpu":

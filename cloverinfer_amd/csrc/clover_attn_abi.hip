@@ -539,6 +539,28 @@ int clv_paged_decode_append(const clv_decode_args *a, const void *key_new, const
   return clv::launch_stream_reduce(p, (DType)a->dtype, s) == hipSuccess ? CLV_OK : CLV_ELAUNCH;
 }
 
+int clv_balanced_reduce_append(const clv_decode_args *a, const void *key_new,
+                               const void *value_new, int64_t new_stride_seq,
+                               int64_t new_stride_head, const int64_t *slot_mapping,
+                               int32_t num_waves, const void *workspace, size_t workspace_bytes,
+                               clv_stream_t stream) {
+  clv::DecodeParams p;
+  const int st = fill_balanced(a, num_waves, const_cast<void *>(workspace), workspace_bytes, &p);
+  if (st != CLV_OK || p.num_seqs == 0) return st;
+  const int eb = elem_bytes(a->dtype);
+  if (!key_new || !value_new || !slot_mapping || !aligned16(key_new) || !aligned16(value_new) ||
+      !stride16(new_stride_seq, eb) || !stride16(new_stride_head, eb))
+    return CLV_EINVAL;
+  p.key_new = key_new;
+  p.value_new = value_new;
+  p.new_stride_seq = new_stride_seq;
+  p.new_stride_head = new_stride_head;
+  p.slot_mapping = slot_mapping;
+  return clv::launch_stream_reduce_append(p, (DType)a->dtype, (hipStream_t)stream) == hipSuccess
+             ? CLV_OK
+             : CLV_ELAUNCH;
+}
+
 int clv_paged_decode_fp8(const clv_decode_args *a, const float *k_scales, const float *v_scales,
                          int32_t num_waves, void *workspace, size_t workspace_bytes,
                          clv_stream_t stream) {

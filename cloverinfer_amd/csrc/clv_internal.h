@@ -50,6 +50,10 @@ struct DecodeParams {
   const void *key_new;
   const void *value_new;
   int64_t new_stride_seq, new_stride_head;
+  // Merge with the new token (stream_reduce_append): sequence s's new rows
+  // are written at slot_mapping[s] (block * block_size + offset; negative:
+  // not written), and attended from key_new/value_new themselves.
+  const int64_t *slot_mapping;
   // fp8 pools (balanced mode): k_cache/v_cache hold OCP e4m3 bytes, strides
   // in bytes, with one scale per kv head; q and out are f16/bf16.
   int32_t kv_fp8;
@@ -102,6 +106,9 @@ hipError_t launch_decode_valu(const DecodeParams &p, DType dt, hipStream_t strea
 hipError_t launch_splitk_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_decode_stream(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_stream_reduce(const DecodeParams &p, DType dt, hipStream_t stream);
+// stream_reduce over partials of context_lens[s] tokens plus sequence s's new
+// token (key_new/value_new[s]), which it also writes at slot_mapping[s].
+hipError_t launch_stream_reduce_append(const DecodeParams &p, DType dt, hipStream_t stream);
 hipError_t launch_prefill_mfma(const PrefillParams &p, DType dt, hipStream_t stream);
 // Writes key_new/value_new[s] at position context_lens[s] - 1 of every
 // sequence (slot from its block table), for the decode shapes whose stream

@@ -669,9 +669,14 @@ struct StreamWave<float, D, UNI, false> {
 // round so that their latencies overlap (R = 16 for NW > 1: 64 partitions
 // then take one round per wave). NW > 1 combines the waves through smem
 // (NW * (D + 1) floats) and needs every thread of the workgroup to call this.
+// An extra row of max xm, sum 1 and context xv (element lane + 64 e in
+// xv[e]) joins the merge when xm is not -inf: a single token's own term
+// (score xm, value xv), so that a decode over a context can take one more
+// token after its partials are written.
 template <typename T, int D, int NW>
 __device__ __forceinline__ void lse_merge(const float *m, const float *l, const float *c,
-                                          int64_t ms, int64_t cs, int n, T *dst, float *smem) {
+                                          int64_t ms, int64_t cs, int n, T *dst, float *smem,
+                                          float xm = kNegInf, const float *xv = nullptr) {
   constexpr int EPL = (D + 63) / 64;
   constexpr int R = NW > 1 ? 16 : 8;
   const int lane = threadIdx.x & 63;
@@ -693,7 +698,7 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
 #pragma unroll
     for (int e = 0; e < EPL; ++e)
       v[u][e] = (u < cnt0 && lane + 64 * e < D) ? c[(int64_t)(base0 + u) * cs + lane + 64 * e] : 0.f;
-  float M = m0;
+  float M = fmaxf(m0, xm);
   for (int i = lane; i < n; i += 64)
     if (i < base0 || i >= base0 + cnt0) M = fmaxf(M, m[i * ms]);
 #pragma unroll
@@ -752,6 +757,12 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
 #pragma unroll
         for (int w = 0; w < NW; ++w) acc[e] += sa[w * D + lane + 64 * e];
     }
+  }
+  if (xm != kNegInf) {  // the extra row, after the waves are combined
+    const float wx = fast_exp2((xm - Msub) * kLog2e);
+    L += wx;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += xv[e] * wx;
   }
   const float inv = 1.f / fmaxf(L, 1e-12f);
 #pragma unroll

@@ -250,7 +250,14 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
 }
 
 // One wave per (sequence, query head).
-template <typename T, int D>
+// NEW: the partials cover context_lens[s] tokens and the merge takes
+// sequence s's new token as one more row: score q[s, h] . key_new[s, kvh]
+// in the scale of the partials (fp32 products of the 16-bit values, as the
+// score MFMAs form them), sum 1, context value_new[s, kvh]. The wave of the
+// kv head's first query head also writes the token's key and value rows at
+// slot_mapping[s] (skipped when negative or past the pools), for the decode
+// steps after this one.
+template <typename T, int D, bool NEW = false>
 __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (idx >= (int64_t)p.num_seqs * p.num_heads) return;
@@ -269,8 +276,54 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
   const int64_t row0 = (n > 0 ? (((int64_t)seg + wave_of(a, W, N)) * HG + wk) * 16 : 0) + g;
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
-  lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
-                     dst, nullptr);
+  if constexpr (!NEW) {
+    lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
+                       dst, nullptr);
+  } else {
+    constexpr int EPL = (D + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    const T *qr = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)h * p.q_stride_head;
+    const int64_t nrow = (int64_t)s * p.new_stride_seq + (int64_t)kvh * p.new_stride_head;
+    const T *kr = (const T *)p.key_new + nrow;
+    const T *vr = (const T *)p.value_new + nrow;
+    T kx[EPL], vx[EPL];
+    float xv[EPL];
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int d = lane + 64 * e;
+      xv[e] = 0.f;
+      if (d < D) {
+        kx[e] = kr[d];
+        vx[e] = vr[d];
+        dot += to_f32(qr[d]) * to_f32(kx[e]);
+        xv[e] = to_f32(vx[e]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) dot += shfl_xor(dot, off);
+    if (gall == 0) {
+      const int64_t slot = p.slot_mapping[s];
+      if (slot >= 0 && slot < ((int64_t)p.num_blocks << p.block_shift)) {
+        const int64_t o = (slot >> p.block_shift) * p.kv_stride_block +
+                          (slot & ((1 << p.block_shift) - 1)) * p.kv_stride_token +
+                          (int64_t)kvh * p.kv_stride_head;
+        T *kd = (T *)p.k_cache + o;
+        T *vd = (T *)p.v_cache + o;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const int d = lane + 64 * e;
+          if (d < D) {
+            kd[d] = kx[e];
+            vd[d] = vx[e];
+          }
+        }
+      }
+    }
+    // The partials' row maxima are log2-domain scores times ln 2.
+    lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
+                       dst, nullptr, dot * p.scale_log2 * kLn2, xv);
+  }
 }
 
 template <typename T, int D, int DEPTH>
@@ -318,14 +371,14 @@ hipError_t launch_stream_t(const DecodeParams &p, hipStream_t stream) {
   return hipErrorInvalidValue;
 }
 
-template <typename T>
+template <typename T, bool NEW = false>
 hipError_t launch_sreduce_t(const DecodeParams &p, hipStream_t stream) {
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
   const dim3 grid((unsigned)((rows + 3) / 4));
   if (p.head_dim == 128)
-    hipLaunchKernelGGL((stream_reduce<T, 128>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((stream_reduce<T, 128, NEW>), grid, dim3(256), 0, stream, p);
   else if (p.head_dim == 64)
-    hipLaunchKernelGGL((stream_reduce<T, 64>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((stream_reduce<T, 64, NEW>), grid, dim3(256), 0, stream, p);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -355,6 +408,14 @@ hipError_t launch_stream_reduce(const DecodeParams &p, DType dt, hipStream_t str
   if (dt == DType::BF16) return launch_sreduce_t<__bf16>(p, stream);
   if (dt == DType::F16) return launch_sreduce_t<_Float16>(p, stream);
   if (dt == DType::F32) return launch_sreduce_t<float>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_stream_reduce_append(const DecodeParams &p, DType dt, hipStream_t stream) {
+  if (p.kv_fp8) return hipErrorInvalidValue;
+  if (dt == DType::BF16) return launch_sreduce_t<__bf16, true>(p, stream);
+  if (dt == DType::F16) return launch_sreduce_t<_Float16, true>(p, stream);
+  if (dt == DType::F32) return launch_sreduce_t<float, true>(p, stream);
   return hipErrorInvalidValue;
 }
 

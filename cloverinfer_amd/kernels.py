@@ -372,6 +372,96 @@ class AppendDecodeLaunch:
         return call
 
 
+class SplitAppendDecode:
+    """One decode step of the append-then-attend protocol in two launches,
+    for a caller that can start the decode before the new key/value rows are
+    at hand: :meth:`partials` (clv_balanced_partials) attends over the
+    ``context_lens[s]`` cached tokens, :meth:`reduce`
+    (clv_balanced_reduce_append) merges in each sequence's new token and
+    writes its rows at the caller's slots (reshape_and_cache semantics:
+    negative slots are skipped; the block tables need not name the new
+    token's block yet). The output equals :func:`paged_attention_append`'s
+    over ``context_lens + 1`` tokens, up to the fp32 rounding of the new
+    token's score. Built once per batch shape and pointed at each call's
+    buffers with :meth:`update`, like :class:`AppendDecodeLaunch`; the
+    balanced decode's shapes with fp32/fp16/bf16 pools."""
+
+    def __init__(self, out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, block_tables: torch.Tensor, context_lens: torch.Tensor,
+                 block_size: int, max_context_len: int, scale: float | None = None,
+                 num_waves: int = 0):
+        self.device = _require_device(out, q, k_cache, v_cache, block_tables, context_lens)
+        a = _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
+                         max_context_len, scale)
+        if not balanced_supported(a):
+            raise NotImplementedError("the split decode covers the balanced decode's shapes only")
+        self.args = a
+        self.num_waves = num_waves
+        self.new_shape = (a.num_seqs, a.num_kv_heads, a.head_dim)
+        self.cache_dtype = k_cache.dtype
+        lib = _native.load()
+        self.workspace_bytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads,
+                                                                a.num_kv_heads, a.head_dim,
+                                                                num_waves)
+        self._partials_fn = lib.clv_balanced_partials
+        self._reduce_fn = lib.clv_balanced_reduce_append
+        self._ws = None
+
+    def update(self, out: torch.Tensor, q: torch.Tensor, block_tables: torch.Tensor,
+               context_lens: torch.Tensor, max_context_len: int) -> None:
+        """Point the launch at this call's buffers (the shapes and strides of
+        the build; not checked)."""
+        a = self.args
+        a.out, a.q = out.data_ptr(), q.data_ptr()
+        a.block_tables, a.max_blocks_per_seq = block_tables.data_ptr(), block_tables.shape[1]
+        a.context_lens = context_lens.data_ptr()
+        a.max_context_len = int(max_context_len)
+
+    def partials(self, stream: int | None = None) -> None:
+        """The decode over the cached tokens, on the current stream (or the
+        stream handle given)."""
+        if stream is None:
+            stream = _stream(self.device)
+        # The merge reads what this launch writes: it keeps the workspace.
+        self._ws = ws = splitk_workspace(self.device, self.workspace_bytes, stream)
+        _native.check(self._partials_fn(self.args, self.num_waves, ws.data_ptr(), ws.numel(),
+                                        stream), "clv_balanced_partials")
+
+    def reduce(self, key_new: torch.Tensor, value_new: torch.Tensor, slots: torch.Tensor,
+               stream: int | None = None, out_address: int | None = None) -> None:
+        """Merge in sequence s's new token (key_new/value_new[s], [num_kv_heads,
+        head_dim] in the cache dtype) and write its rows at ``slots[s]``
+        (int64); after :meth:`partials` on the same stream. ``out_address``:
+        write the result there instead of the build's output, with that
+        output's strides (for instance the device address of pinned host
+        memory, :func:`_native.mapped_device_address`, so that the result
+        needs no copy back)."""
+        if self._ws is None:
+            raise RuntimeError("reduce() needs the partials of this launch first")
+        if key_new.shape != self.new_shape or value_new.shape != self.new_shape:
+            raise ValueError(f"key_new/value_new must be {self.new_shape}, got "
+                             f"{tuple(key_new.shape)} and {tuple(value_new.shape)}")
+        if key_new.dtype != self.cache_dtype or value_new.dtype != self.cache_dtype:
+            raise ValueError("key_new/value_new dtype must match the cache dtype")
+        if slots.dtype != torch.int64 or slots.dim() != 1 or slots.shape[0] < self.new_shape[0] \
+                or slots.stride(0) != 1:
+            raise ValueError("slots must be a contiguous int64 vector, one slot per sequence")
+        if _require_device(key_new, value_new, slots) != self.device:
+            raise ValueError(f"key_new/value_new/slots must be on {self.device}")
+        key_new, value_new = AppendDecodeLaunch._rows(key_new, value_new)
+        if stream is None:
+            stream = _stream(self.device)
+        ws = self._ws
+        a = self.args
+        if out_address is not None:
+            a = type(a).from_buffer_copy(a)
+            a.out = out_address
+        _native.check(self._reduce_fn(a, key_new.data_ptr(), value_new.data_ptr(),
+                                      key_new.stride(0), key_new.stride(1), slots.data_ptr(),
+                                      self.num_waves, ws.data_ptr(), ws.numel(), stream),
+                      "clv_balanced_reduce_append")
+
+
 def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                            v_cache: torch.Tensor, block_tables: torch.Tensor,
                            context_lens: torch.Tensor, block_size: int, max_context_len: int,
@@ -394,7 +484,13 @@ def paged_attention_append(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Te
 
 def append_fusable(q: torch.Tensor, k_cache: torch.Tensor, num_seqs: int) -> bool:
     """Whether :func:`paged_attention_append` covers this decode shape."""
-    hq, hkv, d = q.shape[1], k_cache.shape[2], k_cache.shape[3]
+    return append_fusable_shape(q.shape[1], k_cache, num_seqs)
+
+
+def append_fusable_shape(num_heads: int, k_cache: torch.Tensor, num_seqs: int) -> bool:
+    """:func:`append_fusable` for ``num_heads`` query heads (also the shapes
+    of :class:`SplitAppendDecode`)."""
+    hq, hkv, d = num_heads, k_cache.shape[2], k_cache.shape[3]
     nseg = num_seqs * hkv * ((hq // hkv + 15) // 16)
     return (k_cache.dtype in (torch.float16, torch.bfloat16, torch.float32) and d in (64, 128)
             and k_cache.shape[1] >= 4 and nseg <= BALANCED_MAX_SEGMENTS)

@@ -258,6 +258,31 @@ int clv_paged_decode_append(const clv_decode_args *args, const void *key_new,
                             clv_stream_t stream);
 
 /*
+ * The same decode step in two launches, for a caller that can start the
+ * decode over the cached context before the new rows are at hand (the node
+ * stages each call's payloads on the host while the GPU works):
+ * clv_balanced_partials(args) over context_lens[s] cached tokens, then this
+ * merge, which attends each sequence's query rows to those tokens plus its
+ * new token (key_new[s], value_new[s]: [num_kv_heads, head_dim], strides in
+ * elements), and writes the new rows at slot_mapping[s] (block * block_size
+ * + offset; no write where negative or at or past num_blocks * block_size)
+ * for the steps after this one. Same args (context_lens = the lengths before
+ * the new token), num_waves and workspace as the partials call; the new
+ * token's score is formed in fp32 from the 16-bit (or fp32) values, so the
+ * result equals clv_paged_decode_append's over context_lens[s] + 1 tokens to
+ * fp32 rounding. The slots are the caller's, as in clv_reshape_and_cache:
+ * the block tables need not hold the new token's block yet. fp32, fp16 and
+ * bf16 pools, the balanced decode's shapes (CLV_EUNSUPPORTED otherwise).
+ * References: CpuAttentionBackend.decode_layer, src/core/attention_backend.py:105-118
+ * (append, then attend); the merge rule of src/core/resident_kv_store.py:2497-2509.
+ */
+int clv_balanced_reduce_append(const clv_decode_args *args, const void *key_new,
+                               const void *value_new, int64_t new_stride_seq,
+                               int64_t new_stride_head, const int64_t *slot_mapping,
+                               int32_t num_waves, const void *workspace,
+                               size_t workspace_bytes, clv_stream_t stream);
+
+/*
  * fp8 KV pools (OCP e4m3, one byte per element, a float32 scale per kv head;
  * the reference keeps its resident KV in fp32 or fp16, the pool dtype knob of
  * src/core/config.py:38, and has no fp8 form). A stored byte b stands for

@@ -283,17 +283,20 @@ def test_packed_batch_equals_item_batch(kv_dtype, dtype):
         b.decode_layer_packed(rids[:2], 0, q[:3], k[:2], v[:2])
 
 
-def test_malformed_payload_leaves_state_unchanged():
+@pytest.mark.parametrize("lens", [[15, 16, 31], [527, 528, 543]], ids=["fused", "split"])
+def test_malformed_payload_leaves_state_unchanged(lens):
     """A decode call with a malformed payload (wrong kv-head count, a query
     whose heads are no multiple of the kv heads, a short key) raises and
     changes nothing: later valid steps, including ones that cross a block
     border and take a new block, still match the restated
-    CpuAttentionBackend, and the context lengths agree."""
+    CpuAttentionBackend, and the context lengths agree. Contexts past 512
+    tokens take the split decode, whose decode over the cached tokens is
+    already queued when a key or value is found malformed."""
     g = torch.Generator().manual_seed(61)
     hq, hkv, d, dtype, bs = 8, 2, 64, torch.bfloat16, 16
-    gpu = GpuAttentionBackend(num_blocks=64, block_size=bs)
+    gpu = GpuAttentionBackend(num_blocks=128, block_size=bs)
     cpu = CpuAttentionOracle()
-    lens = [15, 16, 31]  # each request's next token opens a new block within two steps
+    # each request's next token opens a new block within two steps
     rids = [f"x{i}" for i in range(len(lens))]
     for rid, T in zip(rids, lens):
         kv = [{"key": torch.randn(T, hkv, d, generator=g).to(dtype),

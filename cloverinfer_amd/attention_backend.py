@@ -352,7 +352,14 @@ class GpuAttentionBackend:
         requests = self.requests
         if items:
             # The node's batch: one layer and scale, distinct known requests,
-            # checked with a few C-level passes instead of a loop per item.
+            # checked in one native pass (or a few C-level passes without the
+            # native module) instead of a loop per item.
+            host = _native.load_host()
+            if host is not None and type(items) is list and type(requests) is dict:
+                parsed = host.parse_batch(items, requests)
+                if parsed is not None:
+                    layer, scale, reqs, rows, qs, ks, vs = parsed
+                    return self._run_wave(qs, ks, vs, reqs, int(layer), float(scale), rows=rows)
             layers = set(map(_get_layer, items))
             scales = set(map(_get_scale, items))
             if len(layers) == 1 and len(scales) == 1:
@@ -482,7 +489,7 @@ class GpuAttentionBackend:
         return None
 
     def _run_wave(self, qs, ks, vs, reqs: List[_Request], layer: int, score_scale: float,
-                  packed: bool = False):
+                  packed: bool = False, rows: Optional[np.ndarray] = None):
         """One append + decode over distinct requests. qs / ks / vs: lists of
         per-request payloads, or stacked tensors (packed; returns one tensor).
 
@@ -524,14 +531,10 @@ class GpuAttentionBackend:
         nu_max = self.tables.pending_count() + n
         buf = self._staging("wave", (o_u + 12 * nu_max,), torch.uint8)
         bnp = self._stage_np["wave"]
-        self._filled_host = self._gathered = False
-        q = self._fill(qs, hq, d, dt, buf[:qb])
-        q_host = self._filled_host
-        q_same = self._gathered and dt == q0.dtype  # every query: a host tensor of q0's dtype
-
         # Position of each request's new token in this layer: its cached
         # length (a request whose blocks are full takes one more first).
-        rows = np.fromiter(map(_get_row, reqs), dtype=np.int64, count=n)
+        if rows is None:  # the requests' table rows
+            rows = np.fromiter(map(_get_row, reqs), dtype=np.int64, count=n)
         pos = self._lens[rows, layer]
         narrow = bnp[o_i:o_i + 8 * n].view(np.int32)
         narrow[n:] = rows
@@ -579,7 +582,22 @@ class GpuAttentionBackend:
                          (self._dstage[:o_k], hb[:o_k]), (self._dstage[o_i:o_k], hb[o_i:o_k]),
                          (self._dstage[o_k:e], hb[o_k:e]), (self._dstage[:e], hb[:e]))
                 self._views[vkey] = views
+            self._filled_host = self._gathered = False
+            q = self._fill(qs, hq, d, dt, buf[:qb])
+            q_host = self._filled_host
+            q_same = self._gathered and dt == q0.dtype  # every query: a host tensor of q0's dtype
             q_staged = q is None  # the queries are in the pinned buffer
+            if split:
+                # Upload q, the cached lengths and the rows right away.
+                narrow[:n] = pos
+                dst, src = views[6] if q_staged else views[7]
+                dst.copy_(src, non_blocking=True)
+                h1 = True
+                if self._h1_done is None:
+                    self._h1_done = torch.cuda.Event()
+                    self._up_done = torch.cuda.Event()
+                    self._up_stream = torch.cuda.Stream(device=self.device)
+                self._h1_done.record(stream)
             q = views[0] if q_staged else q
             ctx_dev, rows_dev, slots_dev = views[3], views[4], views[5]
             to_host = (not qs.is_cuda) if packed else (q_host or all(not t.is_cuda for t in qs))
@@ -600,17 +618,7 @@ class GpuAttentionBackend:
 
             launch = None
             if split:
-                # Upload q, the cached lengths and the rows; attend over the
-                # cached tokens.
-                narrow[:n] = pos
-                dst, src = views[6] if q_staged else views[7]
-                dst.copy_(src, non_blocking=True)
-                h1 = True
-                if self._h1_done is None:
-                    self._h1_done = torch.cuda.Event()
-                    self._up_done = torch.cuda.Event()
-                    self._up_stream = torch.cuda.Stream(device=self.device)
-                self._h1_done.record(stream)
+                # Attend over the cached tokens.
                 bt = table()
                 lkey = ("split", n, hq, layer, float(score_scale), dt, q.stride())
                 launch = self._launches.get(lkey)

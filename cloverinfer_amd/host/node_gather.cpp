@@ -1,8 +1,11 @@
-// node_gather.cpp - the "gpu" AttentionNode's payload gather, in native code.
+// node_gather.cpp - the "gpu" AttentionNode's batch check and payload gather,
+// in native code.
 //
-// The node receives a decode batch as one small host tensor per item and
-// payload (query [Hq, D], key and value [Hkv, D], src/core/nodes.py:203-216,
-// src/core/model_adapter.py:382-386); the backend stages all of them in one
+// The node receives a decode batch as a list of item dicts with one small
+// host tensor per payload (query [Hq, D], key and value [Hkv, D],
+// src/core/nodes.py:203-216, src/core/model_adapter.py:382-386); the backend
+// checks that the batch is one layer over distinct requests (parse_batch: one
+// pass over the dicts instead of several), then stages all payloads in one
 // pinned buffer and uploads it with one copy. torch.stack of a list costs
 // about 0.3 us per tensor in its checks and dispatch; this module checks the
 // same properties through torch's C++ API for some tens of nanoseconds per
@@ -12,6 +15,7 @@
 #include <torch/extension.h>
 
 #include <ATen/Parallel.h>
+#include <pybind11/numpy.h>
 
 #include <algorithm>
 #include <cstring>
@@ -67,10 +71,81 @@ bool copy_rows(at::Tensor src, at::Tensor dst) {
   return true;
 }
 
+// The item fields, interned once.
+PyObject *key(const char *name) {
+  PyObject *k = PyUnicode_InternFromString(name);
+  if (k == nullptr) throw py::error_already_set();
+  return k;  // kept for the life of the process
+}
+
+// One pass over a decode batch (a list of item dicts) for the backend's
+// common case: every item of one layer and one score scale (compared as the
+// backend's sets compare them), each naming a distinct known request.
+// Returns (layer, scale, requests, rows, queries, keys, values) with rows an
+// int64 array of the requests' table rows, or None whenever the batch is not
+// that case (an item that is no dict or lacks a field, an unknown request
+// id, two items of one request, mixed layers or scales): the backend's
+// general path then takes it and raises its own errors. Errors raised by the
+// lookups themselves (an unhashable id) propagate.
+py::object parse_batch(py::list items, py::dict requests) {
+  static PyObject *const k_layer = key("layer_idx"), *const k_scale = key("score_scale"),
+                         *const k_rid = key("request_id"), *const k_q = key("query"),
+                         *const k_k = key("key"), *const k_v = key("value"), *const k_row = key("row");
+  PyObject *lst = items.ptr();
+  const Py_ssize_t n = PyList_GET_SIZE(lst);
+  if (n == 0) return py::none();
+  py::list reqs(n), qs(n), ks(n), vs(n);
+  py::array_t<int64_t> rows(n);
+  int64_t *r = rows.mutable_data();
+  py::object one = py::float_(1.0);
+  PyObject *layer0 = nullptr, *scale0 = nullptr;
+  auto get = [](PyObject *d, PyObject *k) {
+    PyObject *x = PyDict_GetItemWithError(d, k);  // borrowed
+    if (x == nullptr && PyErr_Occurred()) throw py::error_already_set();
+    return x;
+  };
+  auto same = [](PyObject *a, PyObject *b) {
+    const int eq = PyObject_RichCompareBool(a, b, Py_EQ);
+    if (eq < 0) throw py::error_already_set();
+    return eq == 1;
+  };
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject *it = PyList_GET_ITEM(lst, i);
+    if (!PyDict_Check(it)) return py::none();
+    PyObject *layer = get(it, k_layer), *scale = get(it, k_scale), *rid = get(it, k_rid);
+    PyObject *q = get(it, k_q), *k = get(it, k_k), *v = get(it, k_v);
+    if (!layer || !rid || !q || !k || !v) return py::none();
+    if (scale == nullptr) scale = one.ptr();
+    if (i == 0) {
+      layer0 = layer;
+      scale0 = scale;
+    } else if (!same(layer, layer0) || !same(scale, scale0)) {
+      return py::none();
+    }
+    PyObject *req = get(requests.ptr(), rid);
+    if (req == nullptr) return py::none();
+    py::object row = py::reinterpret_steal<py::object>(PyObject_GetAttr(req, k_row));
+    if (!row) throw py::error_already_set();
+    const long long rv = PyLong_AsLongLong(row.ptr());
+    if (rv == -1 && PyErr_Occurred()) throw py::error_already_set();
+    r[i] = rv;
+    PyList_SET_ITEM(reqs.ptr(), i, (Py_INCREF(req), req));
+    PyList_SET_ITEM(qs.ptr(), i, (Py_INCREF(q), q));
+    PyList_SET_ITEM(ks.ptr(), i, (Py_INCREF(k), k));
+    PyList_SET_ITEM(vs.ptr(), i, (Py_INCREF(v), v));
+  }
+  std::vector<int64_t> sorted(r, r + n);
+  std::sort(sorted.begin(), sorted.end());
+  if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) return py::none();
+  return py::make_tuple(py::reinterpret_borrow<py::object>(layer0),
+                        py::reinterpret_borrow<py::object>(scale0), reqs, rows, qs, ks, vs);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "payload gather of the gpu AttentionNode backend";
   m.def("gather_rows", &gather_rows, "copy a list of CPU tensors into the rows of dst");
   m.def("copy_rows", &copy_rows, "copy a contiguous CPU tensor into dst in parallel");
+  m.def("parse_batch", &parse_batch, "one pass over a uniform decode batch of item dicts");
 }

@@ -58,3 +58,60 @@ def test_copy_rows(gather):
     for bad in (src.float(), src[:, :, :64], src.transpose(0, 1)):
         out = torch.zeros_like(dst)
         assert not gather.copy_rows(bad, out) and torch.equal(out, torch.zeros_like(dst))
+
+
+class _Req:
+    __slots__ = ("blocks", "row")
+
+    def __init__(self, row):
+        self.blocks, self.row = [], row
+
+
+def test_parse_batch_uniform_and_refusals(gather):
+    """The native one-pass batch check: a batch of one layer and scale over
+    distinct known requests comes back as the backend's Python checks would
+    build it; anything else is refused with None (the backend's general path
+    then takes it), and errors of the lookups themselves propagate."""
+    import numpy as np
+    reqs = {f"r{i}": _Req(7 + 3 * i) for i in range(6)}
+
+    def items(**over):
+        out = [{"request_id": f"r{i}", "layer_idx": 1, "query": torch.randn(2, 4),
+                "key": torch.randn(1, 4), "value": torch.randn(1, 4), "score_scale": 0.25}
+               for i in range(6)]
+        for i, (k, v) in over.items():
+            if v is None:
+                del out[i][k]
+            else:
+                out[i][k] = v
+        return out
+
+    it = items()
+    layer, scale, rq, rows, qs, ks, vs = gather.parse_batch(it, reqs)
+    assert (layer, scale) == (1, 0.25)
+    assert rq == [reqs[x["request_id"]] for x in it]
+    assert rows.dtype == np.int64 and rows.tolist() == [r.row for r in rq]
+    assert all(a is x["query"] and b is x["key"] and c is x["value"]
+               for a, b, c, x in zip(qs, ks, vs, it))
+    nos = [{k: v for k, v in x.items() if k != "score_scale"} for x in it]
+    assert gather.parse_batch(nos, reqs)[1] == 1.0       # the default scale
+    mixed = [dict(x) for x in it]
+    mixed[2]["layer_idx"] = 1.0                            # equal as a set would count it
+    assert gather.parse_batch(mixed, reqs) is not None
+    for what, bad in {
+        "mixed layers": lambda b: b[3].__setitem__("layer_idx", 2),
+        "mixed scales": lambda b: b[0].__setitem__("score_scale", 0.5),
+        "repeated request": lambda b: b[4].__setitem__("request_id", "r1"),
+        "unknown request": lambda b: b[5].__setitem__("request_id", "nope"),
+        "missing value": lambda b: b[1].pop("value"),
+        "missing layer": lambda b: b[1].pop("layer_idx"),
+        "not a dict": lambda b: b.__setitem__(2, ("r2", 1)),
+    }.items():
+        b = [dict(x) for x in it]
+        bad(b)
+        assert gather.parse_batch(b, reqs) is None, what
+    assert gather.parse_batch([], reqs) is None
+    b = [dict(x) for x in it]
+    b[0]["request_id"] = ["unhashable"]
+    with pytest.raises(TypeError):
+        gather.parse_batch(b, reqs)

@@ -913,6 +913,17 @@ def main() -> int:
         return 1
     if args.config == "all":
         result = result_line(args, bench_all(args, ALL), "qwen7b")
+        # The fp8-pool batch and the "gpu" AttentionNode backend's calls ride
+        # along under "configs" (a failure there is recorded, not raised).
+        for name, fn in (("qwen7b_fp8", bench_decode_fp8),
+                         ("node", bench_node),
+                         ("node_packed", lambda a: bench_node(a, packed=True)),
+                         ("node_fp32", lambda a: bench_node(a, "float32"))):
+            log(f"{name}")
+            try:
+                result["configs"][name] = fn(args)
+            except Exception as exc:  # noqa: BLE001 - reported in the JSON line
+                result["configs"][name] = {"error": f"{type(exc).__name__}: {exc}"}
     elif args.config in DECODE_CONFIGS or args.config == "prefill":
         result = result_line(args, bench_all(args, [args.config]), args.config)
     elif args.config == "qwen7b_fp8":

@@ -24,7 +24,8 @@ def test_more_than_one_gpu_is_refused_with_a_message():
 def test_default_bench_line_has_the_contract_fields():
     """The default run: the headline (GQA Qwen2.5-7B decode) at the top, and
     every workload under "configs", each with its step time, HIP-event kernel
-    times, a roofline entry (achieved <= peak) and a CPU baseline."""
+    times, a roofline entry (achieved <= peak) and a CPU baseline; the fp8-pool
+    batch and the AttentionNode backend's calls beside them."""
     print("bench.py default run, --steps 10 --warmup 3 --cpu-budget 0.5", flush=True)
     proc = subprocess.run([sys.executable, BENCH, "--steps", "10", "--warmup", "3",
                            "--cpu-budget", "0.5"], capture_output=True, text=True, timeout=400,
@@ -44,7 +45,18 @@ def test_default_bench_line_has_the_contract_fields():
     # value = algorithmic bytes / wall time per step
     algo = r["config"]["algorithmic_bytes_per_step"]
     assert r["value"] == pytest.approx(algo / (r["ms_per_step"] * 1e-3) / 1e9, rel=1e-6)
-    assert set(r["configs"]) == {"opt125m", "llama7b", "long32k", "prefill", "qwen7b"}
+    extra = {"qwen7b_fp8", "node", "node_packed", "node_fp32"}
+    assert set(r["configs"]) == {"opt125m", "llama7b", "long32k", "prefill", "qwen7b"} | extra
+    # the fp8-pool batch: its own line, roofline and parity; the AttentionNode
+    # backend's calls: wall time per call
+    fp8 = r["configs"].pop("qwen7b_fp8")
+    assert "error" not in fp8, fp8
+    assert 0 < fp8["roofline"]["frac"] <= 1 and fp8["parity"]["within_bar"], fp8
+    assert fp8["parity"]["rows"] == 128
+    for name in ("node", "node_packed", "node_fp32"):
+        e = r["configs"].pop(name)
+        assert "error" not in e, (name, e)
+        assert e["unit"] == "ms" and e["value"] > 0 and e["higher_is_better"] is False, name
     assert r["configs"]["qwen7b"]["value"] == r["value"]
     # OPT-125m: the step is the fused append + single-pass decode; the
     # two-launch form (reshape_and_cache, then the decode) is timed beside it

@@ -669,14 +669,16 @@ struct StreamWave<float, D, UNI, false> {
 // round so that their latencies overlap (R = 16 for NW > 1: 64 partitions
 // then take one round per wave). NW > 1 combines the waves through smem
 // (NW * (D + 1) floats) and needs every thread of the workgroup to call this.
-// An extra row of max xm, sum 1 and context xv (element lane + 64 e in
-// xv[e]) joins the merge when xm is not -inf: a single token's own term
-// (score xm, value xv), so that a decode over a context can take one more
-// token after its partials are written.
-template <typename T, int D, int NW>
+// X: an extra row of max xm, sum 1 and context xv (element lane + 64 e in
+// xv[e]) joins the merge, a single token's own term (score, value), so that
+// a decode over a context can take one more token after its partials are
+// written. The score is xm = (sum over the wave of xdot) * xscale, summed
+// here after the rows' loads are issued so that its shuffles overlap them.
+template <typename T, int D, int NW, bool X = false>
 __device__ __forceinline__ void lse_merge(const float *m, const float *l, const float *c,
                                           int64_t ms, int64_t cs, int n, T *dst, float *smem,
-                                          float xm = kNegInf, const float *xv = nullptr) {
+                                          float xdot = 0.f, float xscale = 0.f,
+                                          const float *xv = nullptr) {
   constexpr int EPL = (D + 63) / 64;
   constexpr int R = NW > 1 ? 16 : 8;
   const int lane = threadIdx.x & 63;
@@ -698,6 +700,12 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
 #pragma unroll
     for (int e = 0; e < EPL; ++e)
       v[u][e] = (u < cnt0 && lane + 64 * e < D) ? c[(int64_t)(base0 + u) * cs + lane + 64 * e] : 0.f;
+  float xm = kNegInf;
+  if constexpr (X) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) xdot += shfl_xor(xdot, off);
+    xm = xdot * xscale;
+  }
   float M = fmaxf(m0, xm);
   for (int i = lane; i < n; i += 64)
     if (i < base0 || i >= base0 + cnt0) M = fmaxf(M, m[i * ms]);
@@ -758,7 +766,7 @@ __device__ __forceinline__ void lse_merge(const float *m, const float *l, const 
         for (int w = 0; w < NW; ++w) acc[e] += sa[w * D + lane + 64 * e];
     }
   }
-  if (xm != kNegInf) {  // the extra row, after the waves are combined
+  if constexpr (X) {  // the extra row, after the waves are combined
     const float wx = fast_exp2((xm - Msub) * kLog2e);
     L += wx;
 #pragma unroll

@@ -259,12 +259,34 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
 // steps after this one.
 template <typename T, int D, bool NEW = false>
 __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
+  constexpr int EPL = (D + 63) / 64;
   const int64_t idx = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (idx >= (int64_t)p.num_seqs * p.num_heads) return;
   const int s = (int)(idx / p.num_heads);
   const int h = (int)(idx - (int64_t)s * p.num_heads);
   const int kvh = h / p.group;
   const int gall = h - kvh * p.group;
+  // NEW: the new token's rows and slot are loaded first; they do not depend
+  // on the partials' layout, so their latency overlaps the lookups below.
+  const int lane = threadIdx.x & 63;
+  T qx[EPL], kx[EPL], vx[EPL];
+  int64_t slot = -1;
+  if constexpr (NEW) {
+    const T *qr = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)h * p.q_stride_head;
+    const int64_t nrow = (int64_t)s * p.new_stride_seq + (int64_t)kvh * p.new_stride_head;
+    const T *kr = (const T *)p.key_new + nrow;
+    const T *vr = (const T *)p.value_new + nrow;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int d = lane + 64 * e;
+      if (d < D) {
+        qx[e] = qr[d];
+        kx[e] = kr[d];
+        vx[e] = vr[d];
+      }
+    }
+    if (gall == 0) slot = p.slot_mapping[s];
+  }
   const int HG = p.head_group;
   const int kvg = kvh / HG, wk = kvh - kvg * HG;
   const int seg = (s * (p.num_kv_heads / HG) + kvg) * p.n_gchunks + gall / 16;
@@ -280,49 +302,36 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
     lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
                        dst, nullptr);
   } else {
-    constexpr int EPL = (D + 63) / 64;
-    const int lane = threadIdx.x & 63;
-    const T *qr = (const T *)p.q + (int64_t)s * p.q_stride_seq + (int64_t)h * p.q_stride_head;
-    const int64_t nrow = (int64_t)s * p.new_stride_seq + (int64_t)kvh * p.new_stride_head;
-    const T *kr = (const T *)p.key_new + nrow;
-    const T *vr = (const T *)p.value_new + nrow;
-    T kx[EPL], vx[EPL];
-    float xv[EPL];
-    float dot = 0.f;
+    // The new token as one more row: its score q . key_new in the scale of
+    // the partials (log2-domain scores times ln 2), fp32 products of the
+    // 16-bit values as the score MFMAs form them, sum 1, context value_new.
+    float xdot = 0.f, xv[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      const int d = lane + 64 * e;
-      xv[e] = 0.f;
-      if (d < D) {
-        kx[e] = kr[d];
-        vx[e] = vr[d];
-        dot += to_f32(qr[d]) * to_f32(kx[e]);
-        xv[e] = to_f32(vx[e]);
-      }
+      const bool in = lane + 64 * e < D;
+      xdot += in ? to_f32(qx[e]) * to_f32(kx[e]) : 0.f;
+      xv[e] = in ? to_f32(vx[e]) : 0.f;
     }
+    lse_merge<T, D, 1, true>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG,
+                             16 * HG * D, n, dst, nullptr, xdot, p.scale_log2 * kLn2, xv);
+    // The kv head's first query head writes the token's rows at its slot,
+    // for the decode steps after this one (after the merge: no load of this
+    // kernel waits behind these stores).
+    if (gall == 0 && slot >= 0 && slot < ((int64_t)p.num_blocks << p.block_shift)) {
+      const int64_t o = (slot >> p.block_shift) * p.kv_stride_block +
+                        (slot & ((1 << p.block_shift) - 1)) * p.kv_stride_token +
+                        (int64_t)kvh * p.kv_stride_head;
+      T *kd = (T *)p.k_cache + o;
+      T *vd = (T *)p.v_cache + o;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) dot += shfl_xor(dot, off);
-    if (gall == 0) {
-      const int64_t slot = p.slot_mapping[s];
-      if (slot >= 0 && slot < ((int64_t)p.num_blocks << p.block_shift)) {
-        const int64_t o = (slot >> p.block_shift) * p.kv_stride_block +
-                          (slot & ((1 << p.block_shift) - 1)) * p.kv_stride_token +
-                          (int64_t)kvh * p.kv_stride_head;
-        T *kd = (T *)p.k_cache + o;
-        T *vd = (T *)p.v_cache + o;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-          const int d = lane + 64 * e;
-          if (d < D) {
-            kd[d] = kx[e];
-            vd[d] = vx[e];
-          }
+      for (int e = 0; e < EPL; ++e) {
+        const int d = lane + 64 * e;
+        if (d < D) {
+          kd[d] = kx[e];
+          vd[d] = vx[e];
         }
       }
     }
-    // The partials' row maxima are log2-domain scores times ln 2.
-    lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,
-                       dst, nullptr, dot * p.scale_log2 * kLn2, xv);
   }
 }
 

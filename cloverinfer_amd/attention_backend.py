@@ -11,15 +11,20 @@ Storage is paged instead of one contiguous tensor per (request, layer):
 per-layer pools ``[num_blocks, block_size, num_kv_heads, head_dim]`` share
 one block table per request, so token p of a request lives in the same slot
 of every layer. A batch of decode items for one layer becomes one
-reshape_and_cache launch plus one paged-decode launch, fed by:
+append-then-attend step on the GPU: a fused append + decode launch for short
+contexts, and for contexts past 512 tokens the decode over the cached tokens,
+started as soon as the queries are uploaded, followed by a merge that takes
+each request's new token and writes its rows. It is fed by:
 
 * a device-resident block table (``DeviceBlockTable``): a request's row is
   written once at ``init_request``; a block taken during decode is one
   queued entry (the reference rebuilds the table on the host every call,
   src/core/memory_manager.py:145-173);
-* one host-to-device copy of the batch's q/k/v rows, staged in pinned
-  memory, and one of its metadata (slots, context lengths, table rows);
-* one device-to-host copy of the batch's outputs.
+* the batch's q/k/v rows and metadata (slots, context lengths, table rows)
+  staged in pinned memory and uploaded in one copy, or in two around the
+  decode's start (the second on a copy stream of its own);
+* one device-to-host copy of the batch's outputs, or none where the merge
+  writes them straight into the pinned tensor the call returns.
 """
 from __future__ import annotations
 
@@ -726,6 +731,8 @@ class GpuAttentionBackend:
                 self.tables.requeue(upd)
             if h1:  # the pinned buffer is read until the first upload is done
                 self._stage_done.record(stream)
+            if direct is not None:  # a merge may be writing the pinned result: let it end
+                stream.synchronize()
             raise
         finally:
             if issued:

@@ -914,14 +914,18 @@ def main() -> int:
     if args.config == "all":
         result = result_line(args, bench_all(args, ALL), "qwen7b")
         # The fp8-pool batch and the "gpu" AttentionNode backend's calls ride
-        # along under "configs" (a failure there is recorded, not raised).
-        for name, fn in (("qwen7b_fp8", bench_decode_fp8),
-                         ("node", bench_node),
-                         ("node_packed", lambda a: bench_node(a, packed=True)),
-                         ("node_fp32", lambda a: bench_node(a, "float32"))):
+        # along under "configs" (a failure there is recorded, not raised). A
+        # node call is a fraction of a millisecond of wall time, noisy over a
+        # few calls: those time at least 200 (after at least 50 warm-up).
+        node_args = argparse.Namespace(**{**vars(args), "steps": max(args.steps, 200),
+                                          "warmup": max(args.warmup, 50)})
+        for name, fn, a in (("qwen7b_fp8", bench_decode_fp8, args),
+                            ("node", bench_node, node_args),
+                            ("node_packed", lambda a: bench_node(a, packed=True), node_args),
+                            ("node_fp32", lambda a: bench_node(a, "float32"), node_args)):
             log(f"{name}")
             try:
-                result["configs"][name] = fn(args)
+                result["configs"][name] = fn(a)
             except Exception as exc:  # noqa: BLE001 - reported in the JSON line
                 result["configs"][name] = {"error": f"{type(exc).__name__}: {exc}"}
     elif args.config in DECODE_CONFIGS or args.config == "prefill":

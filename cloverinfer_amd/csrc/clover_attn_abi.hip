@@ -393,6 +393,21 @@ int stream_depth_setting(int def) {
 static_assert(CLV_STREAM_RUN_COST >= 0 && CLV_STREAM_RUN_COST <= 64, "run cost 0..64 steps");
 constexpr int kStreamRunCost = CLV_STREAM_RUN_COST;
 
+// Steps of a first-slot group of the balanced decode against one of a
+// second-slot group, times 256, when the grid is two workgroups per compute
+// unit (see StreamSplit in decode_stream.hip); 256 is the even split.
+// fp8 GQA-7B batch (2048 waves), wave end times read from the realtime
+// counter: at 256 the second-slot waves end 5.3 us after the first-slot
+// ones on average, at 282 (1.10) both slots end within 0.5 us of each other,
+// the launch span falls from 87.5 to 86.7 us and back-to-back launches from
+// 91.2-92.0 to 89.3-90.3 us; 320 and 345 are slower than 256. Fixed at
+// build time (preprocessor value CLV_STREAM_SKEW_Q8).
+#ifndef CLV_STREAM_SKEW_Q8
+#define CLV_STREAM_SKEW_Q8 282
+#endif
+static_assert(CLV_STREAM_SKEW_Q8 >= 128 && CLV_STREAM_SKEW_Q8 <= 512, "weight 0.5..2");
+constexpr int kStreamSkewQ8 = CLV_STREAM_SKEW_Q8;
+
 // kv heads that one workgroup of the balanced decode reads together (one
 // wave each): all of them up to four (a token's whole row of the pools; GQA-7B
 // batch, 4 kv heads: 175.3 -> 173.1 us), else pairs (MHA Llama-7B batch, 32
@@ -435,6 +450,14 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   p->stream_depth = stream_depth_setting(a->dtype == CLV_F32 ? 2 : 3);
   p->stream_run_cost = kStreamRunCost;
   p->num_segments = (int32_t)(nseg / hg);
+  // Two workgroups (of four waves) per compute unit: the first-dispatched
+  // slot takes the larger piece of the split (decode_stream.hip,
+  // StreamSplit). Partials and merge derive the same split from num_waves.
+  const int cus = device_compute_units();
+  if (kStreamSkewQ8 != 256 && num_waves == 2 * 4 * cus) {
+    p->skew_groups = 4 * cus / hg;
+    p->skew_q8 = kStreamSkewQ8;
+  }
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);
   p->ws_m = (float *)ws;

@@ -42,6 +42,11 @@ struct DecodeParams {
   int32_t stream_run_cost;  // phantom steps charged for each segment start (see decode_stream.hip)
   int32_t num_segments;   // num_seqs * (num_kv_heads / head_group) * n_gchunks
   int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
+  // Two-piece split (see decode_stream.hip): groups [0, skew_groups) share a
+  // larger piece of the steps, each weighted skew_q8 / 256 against the other
+  // groups' 1; skew_groups 0 is the even split.
+  int32_t skew_groups;
+  int32_t skew_q8;
   // Fused append (balanced mode): when append_new is set, sequence s's new
   // key/value rows key_new/value_new[s] ([num_kv_heads, head_dim], strides in
   // elements) are written at its context position context_lens[s] - 1 by the

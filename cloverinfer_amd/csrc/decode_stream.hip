@@ -6,6 +6,7 @@
 //   (sequence, kv head, query-head chunk, step)    -- one "segment" per
 // (sequence, kv head, chunk), N steps in total
 // evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders
+// (or in two even pieces at two workgroups per compute unit: StreamSplit)
 // (W is capped at N, so no wave is idle and a segment's partials come from
 // consecutive waves).
 // Each wave keeps a ring of steps of loads in flight and, for every segment it
@@ -38,15 +39,44 @@ namespace {
 constexpr int kWaves = 4;  // independent waves per workgroup
 constexpr int kThreads = kWaves * 64;
 
-// Wave owning step x when N steps are split over W waves: the largest w
-// with floor(w*N/W) <= x.
-__device__ __forceinline__ int wave_of(int x, int64_t W, int64_t N) {
-  return (int)(((int64_t)(x + 1) * W - 1) / N);
-}
-
-__device__ __forceinline__ int span_start(int w, int64_t W, int64_t N) {
-  return (int)((int64_t)w * N / W);
-}
+// The split of N steps over W groups (N >= W). Even: group w starts at
+// floor(w*N/W). Two pieces (skew_groups = Wa, 0 < Wa < W): groups [0, Wa)
+// split the first Na steps evenly and groups [Wa, W) the other N - Na, with
+// Na = N * Wa*q / (Wa*q + (W-Wa)*256) for the weight q = skew_q8, held in
+// [Wa, N - (W-Wa)] so that every group owns at least one step.
+//
+// Why two pieces: when the grid is two workgroups per compute unit, the
+// workgroups [0, CUs) are dispatched first, one per CU, and [CUs, 2*CUs)
+// into the second slot, so each SIMD runs one wave of each. The SIMD's issue
+// arbiter favours the older wave: with equal spans it ends first on every
+// SIMD (fp8 GQA-7B batch, 2048 waves: 5.3 us before its partner on average),
+// and the younger wave then runs its last steps alone, at the lower rate of
+// one wave per SIMD. Giving the older slot more steps lets the pair end
+// together.
+struct StreamSplit {
+  int64_t W, N, Wa, Na;
+  __device__ StreamSplit(const DecodeParams &p, int64_t W_, int64_t N_)
+      : W(W_), N(N_), Wa(0), Na(0) {
+    if (p.skew_groups > 0 && p.skew_groups < W) {
+      Wa = p.skew_groups;
+      const int64_t wb = W - Wa;
+      const int64_t na = N * Wa * p.skew_q8 / (Wa * p.skew_q8 + wb * 256);
+      Na = min(max(na, Wa), N - wb);
+    }
+  }
+  // First step of group w (w <= W; start(W) = N).
+  __device__ __forceinline__ int start(int w) const {
+    if (Wa == 0) return (int)((int64_t)w * N / W);
+    if (w < Wa) return (int)((int64_t)w * Na / Wa);
+    return (int)(Na + (int64_t)(w - Wa) * (N - Na) / (W - Wa));
+  }
+  // Group owning step x (0 <= x < N): the largest w with start(w) <= x.
+  __device__ __forceinline__ int owner(int x) const {
+    if (Wa == 0) return (int)(((int64_t)(x + 1) * W - 1) / N);
+    if (x < Na) return (int)(((int64_t)(x + 1) * Wa - 1) / Na);
+    return (int)(Wa + ((int64_t)(x - Na + 1) * (W - Wa) - 1) / (N - Na));
+  }
+};
 
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
@@ -119,8 +149,9 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   const int wid = wv / HG;      // group
   const int wk = wv - wid * HG;  // kv head within the group
   if (N == 0 || wid >= W) return;
-  const int st = span_start(wid, W, N);
-  const int en = span_start(wid + 1, W, N);
+  const StreamSplit split(p, W, N);
+  const int st = split.start(wid);
+  const int en = split.start(wid + 1);
   if (st >= en) return;
 
   // Segment holding step st: the last one whose first step is <= st.
@@ -294,9 +325,13 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int a = p.seg_prefix[seg] + p.stream_run_cost, b = p.seg_prefix[seg + 1];
   const int64_t N = p.seg_prefix[p.num_segments];
   const int64_t W = min((int64_t)(p.num_waves / HG), N);
-  int n = 0;
-  if (b > a) n = wave_of(b - 1, W, N) - wave_of(a, W, N) + 1;
-  const int64_t row0 = (n > 0 ? (((int64_t)seg + wave_of(a, W, N)) * HG + wk) * 16 : 0) + g;
+  int n = 0, w0 = 0;
+  if (b > a) {
+    const StreamSplit split(p, W, N);
+    w0 = split.owner(a);
+    n = split.owner(b - 1) - w0 + 1;
+  }
+  const int64_t row0 = (n > 0 ? (((int64_t)seg + w0) * HG + wk) * 16 : 0) + g;
   T *dst = (T *)p.out + (int64_t)s * p.out_stride_seq + (int64_t)h * p.out_stride_head;
   if constexpr (!NEW) {
     lse_merge<T, D, 1>(p.ws_m + row0, p.ws_l + row0, p.ws_o + row0 * D, 16 * HG, 16 * HG * D, n,

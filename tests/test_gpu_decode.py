@@ -77,6 +77,24 @@ def test_balanced_decode_wave_counts(num_waves, dtype):
     assert torch.equal(got[0].float(), torch.zeros(28, 128))
 
 
+@pytest.mark.parametrize("ctx", [
+    [0, 3000, 17, 811, 0, 4096, 256, 1500, 33, 2222] * 4,  # both pieces long
+    [480] * 10,     # 340 steps: the first piece held at one step per group
+    [200] * 10,     # 170 steps: fewer than the first piece's groups, even split
+], ids=["ragged", "clamped", "even"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_balanced_decode_two_workgroups_per_cu(ctx, dtype):
+    """At two workgroups per compute unit the balanced decode splits the
+    steps in two pieces (the first-dispatched workgroups take the larger
+    one); the merge must find every segment's partials under that split."""
+    waves = 2 * kernels._native.load().clv_default_num_waves()
+    print(f"balanced two-slot waves={waves} dtype={dtype} nseq={len(ctx)}", flush=True)
+    q, k, v, tables, scale = case(len(ctx) + 5, ctx, 28, 4, 128, 16, dtype)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=None, num_waves=waves)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    assert_attention_close(got, ref, what=f"balanced W={waves}")
+
+
 @pytest.mark.parametrize("d,bs", [(128, 16), (64, 16), (128, 8), (64, 4)])
 def test_fp32_balanced_decode_is_fp32_exact(d, bs):
     """fp32 pools on the fp32 MFMA wave: nothing is rounded below fp32, so

@@ -156,3 +156,41 @@ def test_mapped_device_address_and_direct_results():
     ref = oa.paged_decode(q.cpu(), kd.cpu(), vd.cpu(), tables, [c + 1 for c in ctx],
                           1.0 / math.sqrt(d))
     assert_attention_close(host, ref, what="merge into pinned host memory")
+
+
+def test_split_append_two_workgroups_per_cu():
+    """The split step at two workgroups per compute unit, where the balanced
+    decode splits its steps in two pieces: the merge with the new token must
+    find every segment's partials under that split (against the fused step
+    at the same wave count and the oracle)."""
+    hq, hkv, d, bs, dtype = 28, 4, 128, 16, torch.bfloat16
+    ctx = [3000, 17, 811, 0, 4096, 256, 1500, 33] * 3
+    waves = 2 * kernels._native.load().clv_default_num_waves()
+    print(f"split append two-slot waves={waves}", flush=True)
+    k, v, tables = make_paged_kv(31, [c + 1 for c in ctx], hkv, d, bs, dtype)
+    ks, vs = k.to(DEV), v.to(DEV)
+    kf, vf = k.clone().to(DEV), v.clone().to(DEV)
+    bt = padded_tables(tables).to(DEV)
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(len(ctx), hq, d, generator=g).to(dtype).to(DEV)
+    kn = torch.randn(len(ctx), hkv, d, generator=g).to(dtype).to(DEV)
+    vn = torch.randn(len(ctx), hkv, d, generator=g).to(dtype).to(DEV)
+    slots = torch.tensor([t[c // bs] * bs + c % bs for t, c in zip(tables, ctx)],
+                         dtype=torch.int64, device=DEV)
+    new = [c + 1 for c in ctx]
+    scale = 1.0 / math.sqrt(d)
+    out_s = torch.empty_like(q)
+    sp = kernels.SplitAppendDecode(out_s, q, ks, vs, bt, torch.tensor(ctx, dtype=torch.int32,
+                                                                      device=DEV),
+                                   bs, max(ctx), scale=scale, num_waves=waves)
+    sp.partials()
+    sp.reduce(kn, vn, slots)
+    out_f = torch.empty_like(q)
+    kernels.paged_attention_append(out_f, q, kf, vf, bt,
+                                   torch.tensor(new, dtype=torch.int32, device=DEV), bs,
+                                   max(new), kn, vn, scale=scale, num_waves=waves)
+    torch.cuda.synchronize()
+    assert _same_bits(ks, kf) and _same_bits(vs, vf)
+    ref = oa.paged_decode(q.cpu(), ks.cpu(), vs.cpu(), tables, new, scale)
+    assert_attention_close(out_s.cpu(), ref, what="split, two slots")
+    assert_attention_close(out_f.cpu(), ref, what="fused, two slots")

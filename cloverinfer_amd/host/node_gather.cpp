@@ -98,7 +98,7 @@ py::object parse_batch(py::list items, py::dict requests) {
   py::array_t<int64_t> rows(n);
   int64_t *r = rows.mutable_data();
   py::object one = py::float_(1.0);
-  PyObject *layer0 = nullptr, *scale0 = nullptr;
+  py::object layer0, scale0;  // owned: the comparisons below may run Python code
   auto get = [](PyObject *d, PyObject *k) {
     PyObject *x = PyDict_GetItemWithError(d, k);  // borrowed
     if (x == nullptr && PyErr_Occurred()) throw py::error_already_set();
@@ -117,9 +117,9 @@ py::object parse_batch(py::list items, py::dict requests) {
     if (!layer || !rid || !q || !k || !v) return py::none();
     if (scale == nullptr) scale = one.ptr();
     if (i == 0) {
-      layer0 = layer;
-      scale0 = scale;
-    } else if (!same(layer, layer0) || !same(scale, scale0)) {
+      layer0 = py::reinterpret_borrow<py::object>(layer);
+      scale0 = py::reinterpret_borrow<py::object>(scale);
+    } else if (!same(layer, layer0.ptr()) || !same(scale, scale0.ptr())) {
       return py::none();
     }
     PyObject *req = get(requests.ptr(), rid);
@@ -137,8 +137,7 @@ py::object parse_batch(py::list items, py::dict requests) {
   std::vector<int64_t> sorted(r, r + n);
   std::sort(sorted.begin(), sorted.end());
   if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) return py::none();
-  return py::make_tuple(py::reinterpret_borrow<py::object>(layer0),
-                        py::reinterpret_borrow<py::object>(scale0), reqs, rows, qs, ks, vs);
+  return py::make_tuple(layer0, scale0, reqs, rows, qs, ks, vs);
 }
 
 }  // namespace

@@ -27,6 +27,10 @@ DEFAULT_PARTITION = 512
 
 _ws_lock = threading.Lock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Hand-outs of each stream's workspace so far: a launch that keeps partials in
+# it between two calls (SplitAppendDecode) can tell whether another launch
+# took the same buffer in between.
+_ws_epochs: dict[tuple[int, int], int] = {}
 _num_cus: dict[int, int] = {}
 
 
@@ -118,6 +122,12 @@ def splitk_workspace(dev: torch.device, nbytes: int, stream: int | None = None) 
     current stream of ``dev`` (one per stream, so that launches on different
     streams never share partials); ``stream``: that stream's handle, when the
     caller has looked it up already."""
+    return _workspace_lease(dev, nbytes, stream)[0]
+
+
+def _workspace_lease(dev: torch.device, nbytes: int, stream: int | None = None):
+    """:func:`splitk_workspace` plus the (stream key, hand-out count) that
+    :func:`_workspace_reused` checks."""
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     key = (idx, stream if stream is not None else _stream(torch.device("cuda", idx)))
     with _ws_lock:
@@ -125,7 +135,15 @@ def splitk_workspace(dev: torch.device, nbytes: int, stream: int | None = None) 
         if ws is None or ws.numel() < nbytes:
             ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
             _workspaces[key] = ws
-    return ws
+        epoch = _ws_epochs[key] = _ws_epochs.get(key, 0) + 1
+    return ws, key, epoch
+
+
+def _workspace_reused(ws: torch.Tensor, key, epoch: int) -> bool:
+    """Whether the stream's workspace ``ws``, leased at ``epoch``, has been
+    handed out again since (a grown, different buffer leaves ``ws`` alone)."""
+    with _ws_lock:
+        return _workspaces.get(key) is ws and _ws_epochs.get(key) != epoch
 
 
 def _decode_args(out, q, k_cache, v_cache, block_tables, context_lens, block_size,
@@ -384,7 +402,10 @@ class SplitAppendDecode:
     over ``context_lens + 1`` tokens, up to the fp32 rounding of the new
     token's score. Built once per batch shape and pointed at each call's
     buffers with :meth:`update`, like :class:`AppendDecodeLaunch`; the
-    balanced decode's shapes with fp32/fp16/bf16 pools."""
+    balanced decode's shapes with fp32/fp16/bf16 pools. The partials live in
+    the stream's workspace, which every decode of this module on that stream
+    uses: between :meth:`partials` and :meth:`reduce` run no other decode
+    call on the same stream (:meth:`reduce` raises if one ran)."""
 
     def __init__(self, out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
                  v_cache: torch.Tensor, block_tables: torch.Tensor, context_lens: torch.Tensor,
@@ -422,10 +443,14 @@ class SplitAppendDecode:
         stream handle given)."""
         if stream is None:
             stream = _stream(self.device)
-        # The merge reads what this launch writes: it keeps the workspace.
-        self._ws = ws = splitk_workspace(self.device, self.workspace_bytes, stream)
+        # The merge reads what this launch writes: it keeps the workspace
+        # (the stream's, which any other decode of this module on the same
+        # stream also takes: reduce() checks that none did in between).
+        ws, key, epoch = _workspace_lease(self.device, self.workspace_bytes, stream)
+        self._ws = None
         _native.check(self._partials_fn(self.args, self.num_waves, ws.data_ptr(), ws.numel(),
                                         stream), "clv_balanced_partials")
+        self._ws, self._ws_lease = ws, (key, epoch)
 
     def reduce(self, key_new: torch.Tensor, value_new: torch.Tensor, slots: torch.Tensor,
                stream: int | None = None, out_address: int | None = None) -> None:
@@ -438,6 +463,9 @@ class SplitAppendDecode:
         needs no copy back)."""
         if self._ws is None:
             raise RuntimeError("reduce() needs the partials of this launch first")
+        if _workspace_reused(self._ws, *self._ws_lease):
+            raise RuntimeError("another decode on this stream took the workspace that holds "
+                               "this launch's partials: call partials() again before reduce()")
         if key_new.shape != self.new_shape or value_new.shape != self.new_shape:
             raise ValueError(f"key_new/value_new must be {self.new_shape}, got "
                              f"{tuple(key_new.shape)} and {tuple(value_new.shape)}")

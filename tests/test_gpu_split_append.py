@@ -194,3 +194,39 @@ def test_split_append_two_workgroups_per_cu():
     ref = oa.paged_decode(q.cpu(), ks.cpu(), vs.cpu(), tables, new, scale)
     assert_attention_close(out_s.cpu(), ref, what="split, two slots")
     assert_attention_close(out_f.cpu(), ref, what="fused, two slots")
+
+
+def test_split_append_workspace_taken_in_between():
+    """The partials live in the stream's workspace until the merge: another
+    decode on the same stream in between makes reduce() raise instead of
+    merging overwritten partials; a decode on another stream, or partials()
+    run again, do not."""
+    hq, hkv, d, bs, dtype = 28, 4, 128, 16, torch.bfloat16
+    ctx = [700, 600, 900]
+    k, v, tables = make_paged_kv(41, [c + 1 for c in ctx], hkv, d, bs, dtype)
+    kd, vd = k.to(DEV), v.to(DEV)
+    bt = padded_tables(tables).to(DEV)
+    lens = torch.tensor(ctx, dtype=torch.int32, device=DEV)
+    q = torch.randn(3, hq, d).to(dtype).to(DEV)
+    kn = torch.randn(3, hkv, d).to(dtype).to(DEV)
+    vn = torch.randn(3, hkv, d).to(dtype).to(DEV)
+    slots = torch.tensor([t[c // bs] * bs + c % bs for t, c in zip(tables, ctx)],
+                         dtype=torch.int64, device=DEV)
+    out = torch.empty_like(q)
+    other = torch.empty_like(q)
+    sp = kernels.SplitAppendDecode(out, q, kd, vd, bt, lens, bs, max(ctx))
+    sp.partials()
+    kernels.paged_attention(other, q, kd, vd, bt, lens, bs, max(ctx), num_waves=1024)
+    with pytest.raises(RuntimeError, match="workspace"):
+        sp.reduce(kn, vn, slots)
+    sp.partials()  # again: its own lease
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # another stream has its own workspace
+        kernels.paged_attention(other, q, kd, vd, bt, lens, bs, max(ctx), num_waves=1024)
+    torch.cuda.current_stream().wait_stream(side)
+    sp.reduce(kn, vn, slots)
+    torch.cuda.synchronize()
+    ref = oa.paged_decode(q.cpu(), kd.cpu(), vd.cpu(), tables, [c + 1 for c in ctx],
+                          1.0 / math.sqrt(d))
+    assert_attention_close(out.cpu(), ref, what="merge after a decode on another stream")

@@ -393,20 +393,37 @@ int stream_depth_setting(int def) {
 static_assert(CLV_STREAM_RUN_COST >= 0 && CLV_STREAM_RUN_COST <= 64, "run cost 0..64 steps");
 constexpr int kStreamRunCost = CLV_STREAM_RUN_COST;
 
-// Steps of a first-slot group of the balanced decode against one of a
-// second-slot group, times 256, when the grid is two workgroups per compute
-// unit (see StreamSplit in decode_stream.hip); 256 is the even split.
-// fp8 GQA-7B batch (2048 waves), wave end times read from the realtime
-// counter: at 256 the second-slot waves end 5.3 us after the first-slot
-// ones on average, at 282 (1.10) both slots end within 0.5 us of each other,
-// the launch span falls from 87.5 to 86.7 us and back-to-back launches from
-// 91.2-92.0 to 89.3-90.3 us; 320 and 345 are slower than 256. Fixed at
-// build time (preprocessor value CLV_STREAM_SKEW_Q8).
-#ifndef CLV_STREAM_SKEW_Q8
-#define CLV_STREAM_SKEW_Q8 282
+// Steps per group of each dispatch slot of the balanced decode, times 256
+// against the last slot, when the grid is two or three workgroups (of four
+// waves) per compute unit (see StreamSplit in decode_stream.hip); all 256 is
+// the even split. fp8 GQA-7B batch, wave end times read from the realtime
+// counter: at 2048 waves and equal spans the second-slot waves end 5.3 us
+// after the first-slot ones on average; at 282 (1.10) both slots end within
+// 0.5 us of each other, the launch span falls from 87.5 to 86.7 us and
+// back-to-back launches from 91.2-92.0 to 89.3-90.3 us (320 and 345: slower
+// than 256). At 3072 waves the three slots end at 71.6, 78.8 and 86.4 us on
+// average with equal spans; back to back (another box): 99.3-99.6 us at
+// 256/256, 98.0-98.7 at 282/269, 96.7-97.1 at 300/278, 96.1-96.2 at
+// 320/288, 96.4-96.8 at 345/300 (2048 waves there: 95.4-96.3, and per step
+// 0.0981 against 0.1045 ms, the merge reading more partials, so the fp8
+// default stays at two slots). Fixed at build time (preprocessor values
+// CLV_STREAM_SLOT2_Q8 for the first of two slots, CLV_STREAM_SLOT3_Q8_0 and
+// _1 for the first two of three).
+#ifndef CLV_STREAM_SLOT2_Q8
+#define CLV_STREAM_SLOT2_Q8 282
 #endif
-static_assert(CLV_STREAM_SKEW_Q8 >= 128 && CLV_STREAM_SKEW_Q8 <= 512, "weight 0.5..2");
-constexpr int kStreamSkewQ8 = CLV_STREAM_SKEW_Q8;
+#ifndef CLV_STREAM_SLOT3_Q8_0
+#define CLV_STREAM_SLOT3_Q8_0 320
+#endif
+#ifndef CLV_STREAM_SLOT3_Q8_1
+#define CLV_STREAM_SLOT3_Q8_1 288
+#endif
+static_assert(CLV_STREAM_SLOT2_Q8 >= 128 && CLV_STREAM_SLOT2_Q8 <= 512 &&
+                  CLV_STREAM_SLOT3_Q8_0 >= 128 && CLV_STREAM_SLOT3_Q8_0 <= 512 &&
+                  CLV_STREAM_SLOT3_Q8_1 >= 128 && CLV_STREAM_SLOT3_Q8_1 <= 512,
+              "slot weights 0.5..2");
+constexpr int kSlotQ8[2][3] = {{CLV_STREAM_SLOT2_Q8, 256, 256},
+                               {CLV_STREAM_SLOT3_Q8_0, CLV_STREAM_SLOT3_Q8_1, 256}};
 
 // kv heads that one workgroup of the balanced decode reads together (one
 // wave each): all of them up to four (a token's whole row of the pools; GQA-7B
@@ -450,13 +467,16 @@ int fill_balanced(const clv_decode_args *a, int32_t num_waves, void *workspace,
   p->stream_depth = stream_depth_setting(a->dtype == CLV_F32 ? 2 : 3);
   p->stream_run_cost = kStreamRunCost;
   p->num_segments = (int32_t)(nseg / hg);
-  // Two workgroups (of four waves) per compute unit: the first-dispatched
-  // slot takes the larger piece of the split (decode_stream.hip,
-  // StreamSplit). Partials and merge derive the same split from num_waves.
+  // Two or three workgroups (of four waves) per compute unit: one piece of
+  // the split per dispatch slot, the older slots taking more steps
+  // (decode_stream.hip, StreamSplit). Partials and merge derive the same
+  // split from num_waves.
   const int cus = device_compute_units();
-  if (kStreamSkewQ8 != 256 && num_waves == 2 * 4 * cus) {
-    p->skew_groups = 4 * cus / hg;
-    p->skew_q8 = kStreamSkewQ8;
+  for (int slots = 2; slots <= 3; ++slots) {
+    if (num_waves != slots * 4 * cus) continue;
+    p->slot_count = slots;
+    p->slot_groups = 4 * cus / hg;
+    for (int k = 0; k < slots; ++k) p->slot_q8[k] = kSlotQ8[slots - 2][k];
   }
   p->seg_prefix = (int32_t *)ws;
   ws += round256(((size_t)nseg + 1) * 4);

@@ -42,11 +42,13 @@ struct DecodeParams {
   int32_t stream_run_cost;  // phantom steps charged for each segment start (see decode_stream.hip)
   int32_t num_segments;   // num_seqs * (num_kv_heads / head_group) * n_gchunks
   int32_t *seg_prefix;    // [num_segments + 1] exclusive prefix of steps per segment
-  // Two-piece split (see decode_stream.hip): groups [0, skew_groups) share a
-  // larger piece of the steps, each weighted skew_q8 / 256 against the other
-  // groups' 1; skew_groups 0 is the even split.
-  int32_t skew_groups;
-  int32_t skew_q8;
+  // Split by dispatch slot (see StreamSplit in decode_stream.hip): with
+  // slot_count > 1, groups [k * slot_groups, (k+1) * slot_groups) form piece
+  // k (the last piece takes the groups left), and each group of piece k is
+  // weighted slot_q8[k] / 256; slot_count 0 or 1 is the even split.
+  int32_t slot_count;
+  int32_t slot_groups;
+  int32_t slot_q8[4];
   // Fused append (balanced mode): when append_new is set, sequence s's new
   // key/value rows key_new/value_new[s] ([num_kv_heads, head_dim], strides in
   // elements) are written at its context position context_lens[s] - 1 by the

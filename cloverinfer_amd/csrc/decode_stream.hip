@@ -6,7 +6,8 @@
 //   (sequence, kv head, query-head chunk, step)    -- one "segment" per
 // (sequence, kv head, chunk), N steps in total
 // evenly: wave w takes steps [w*N/W, (w+1)*N/W), crossing segment borders
-// (or in two even pieces at two workgroups per compute unit: StreamSplit)
+// (or in one even piece per dispatch slot at several workgroups per compute
+// unit: StreamSplit)
 // (W is capped at N, so no wave is idle and a segment's partials come from
 // consecutive waves).
 // Each wave keeps a ring of steps of loads in flight and, for every segment it
@@ -40,41 +41,68 @@ constexpr int kWaves = 4;  // independent waves per workgroup
 constexpr int kThreads = kWaves * 64;
 
 // The split of N steps over W groups (N >= W). Even: group w starts at
-// floor(w*N/W). Two pieces (skew_groups = Wa, 0 < Wa < W): groups [0, Wa)
-// split the first Na steps evenly and groups [Wa, W) the other N - Na, with
-// Na = N * Wa*q / (Wa*q + (W-Wa)*256) for the weight q = skew_q8, held in
-// [Wa, N - (W-Wa)] so that every group owns at least one step.
+// floor(w*N/W). By dispatch slot (slot_count = S > 1, slot_groups = Gp):
+// the groups form pieces of Gp consecutive groups (piece k: groups
+// [k*Gp, (k+1)*Gp), the last piece those left below W), each piece's steps
+// split evenly over its groups, and piece k's share of the N steps in
+// proportion to its groups times its weight slot_q8[k], every piece held to
+// at least one step per group.
 //
-// Why two pieces: when the grid is two workgroups per compute unit, the
-// workgroups [0, CUs) are dispatched first, one per CU, and [CUs, 2*CUs)
-// into the second slot, so each SIMD runs one wave of each. The SIMD's issue
-// arbiter favours the older wave: with equal spans it ends first on every
-// SIMD (fp8 GQA-7B batch, 2048 waves: 5.3 us before its partner on average),
-// and the younger wave then runs its last steps alone, at the lower rate of
-// one wave per SIMD. Giving the older slot more steps lets the pair end
-// together.
+// Why: at S workgroups (of four waves) per compute unit, the workgroups
+// [0, CUs) are dispatched first, one per CU, then [CUs, 2*CUs) into the
+// second slot, and so on, so each SIMD runs one wave of each slot. The
+// SIMD's issue arbiter favours older waves: with equal spans the slots end
+// in dispatch order on every SIMD (fp8 GQA-7B batch, 2048 waves: the second
+// slot 5.3 us after the first on average; 3072 waves: 71.6, 78.8 and
+// 86.4 us for the three slots), and the youngest waves run their last steps
+// alone, at the lower rate of one wave per SIMD. Giving the older slots
+// more steps lets every slot end together.
 struct StreamSplit {
-  int64_t W, N, Wa, Na;
-  __device__ StreamSplit(const DecodeParams &p, int64_t W_, int64_t N_)
-      : W(W_), N(N_), Wa(0), Na(0) {
-    if (p.skew_groups > 0 && p.skew_groups < W) {
-      Wa = p.skew_groups;
-      const int64_t wb = W - Wa;
-      const int64_t na = N * Wa * p.skew_q8 / (Wa * p.skew_q8 + wb * 256);
-      Na = min(max(na, Wa), N - wb);
+  static constexpr int kMaxSlots = 4;
+  int64_t W, N, Gp;
+  int S;
+  int64_t b1, b2, b3;  // first steps of pieces 1..3 (N past the last piece)
+  __host__ __device__ StreamSplit(const DecodeParams &p, int64_t W_, int64_t N_)
+      : W(W_), N(N_), Gp(p.slot_groups), S(1), b1(N_), b2(N_), b3(N_) {
+    if (p.slot_count > 1 && Gp > 0 && Gp < W) {
+      S = (int)min((int64_t)min(p.slot_count, kMaxSlots), (W + Gp - 1) / Gp);
+      const int64_t w0 = groups(0) * p.slot_q8[0], w1 = groups(1) * p.slot_q8[1];
+      const int64_t w2 = S > 2 ? groups(2) * p.slot_q8[2] : 0;
+      const int64_t w3 = S > 3 ? groups(3) * p.slot_q8[3] : 0;
+      const int64_t total = w0 + w1 + w2 + w3;
+      // Piece k ends at its weighted share, held to at least one step per
+      // group of this piece and of every later one.
+      auto cut = [&](int k, int64_t acc, int64_t prev) {
+        return min(max(N * acc / total, prev + groups(k)), N - (W - (int64_t)(k + 1) * Gp));
+      };
+      b1 = cut(0, w0, 0);
+      if (S > 2) b2 = cut(1, w0 + w1, b1);
+      if (S > 3) b3 = cut(2, w0 + w1 + w2, b2);
     }
   }
+  // Groups of piece k.
+  __host__ __device__ __forceinline__ int64_t groups(int k) const {
+    return k + 1 < S ? Gp : W - (int64_t)k * Gp;
+  }
+  // First step of piece k (0 <= k <= S; N for k >= S).
+  __host__ __device__ __forceinline__ int64_t base(int k) const {
+    return k <= 0 ? 0 : k == 1 ? b1 : k == 2 ? b2 : k == 3 ? b3 : N;
+  }
   // First step of group w (w <= W; start(W) = N).
-  __device__ __forceinline__ int start(int w) const {
-    if (Wa == 0) return (int)((int64_t)w * N / W);
-    if (w < Wa) return (int)((int64_t)w * Na / Wa);
-    return (int)(Na + (int64_t)(w - Wa) * (N - Na) / (W - Wa));
+  __host__ __device__ __forceinline__ int start(int w) const {
+    if (S == 1) return (int)((int64_t)w * N / W);
+    if (w >= W) return (int)N;
+    const int k = (int)min((int64_t)w / Gp, (int64_t)S - 1);
+    const int64_t lo = base(k);
+    return (int)(lo + (w - (int64_t)k * Gp) * (base(k + 1) - lo) / groups(k));
   }
   // Group owning step x (0 <= x < N): the largest w with start(w) <= x.
-  __device__ __forceinline__ int owner(int x) const {
-    if (Wa == 0) return (int)(((int64_t)(x + 1) * W - 1) / N);
-    if (x < Na) return (int)(((int64_t)(x + 1) * Wa - 1) / Na);
-    return (int)(Wa + ((int64_t)(x - Na + 1) * (W - Wa) - 1) / (N - Na));
+  __host__ __device__ __forceinline__ int owner(int x) const {
+    if (S == 1) return (int)(((int64_t)(x + 1) * W - 1) / N);
+    const int k = (S > 3 && b3 <= x) ? 3 : (S > 2 && b2 <= x) ? 2 : b1 <= x ? 1 : 0;
+    const int64_t lo = base(k);
+    return (int)((int64_t)k * Gp +
+                 ((int64_t)(x - lo + 1) * groups(k) - 1) / (base(k + 1) - lo));
   }
 };
 
@@ -150,8 +178,8 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   const int wk = wv - wid * HG;  // kv head within the group
   if (N == 0 || wid >= W) return;
   const StreamSplit split(p, W, N);
-  const int st = split.start(wid);
-  const int en = split.start(wid + 1);
+  const int st = uni(split.start(wid));
+  const int en = uni(split.start(wid + 1));
   if (st >= en) return;
 
   // Segment holding step st: the last one whose first step is <= st.

@@ -188,7 +188,10 @@ int clv_splitk_reduce(const clv_decode_args *args, int32_t partition_size,
  * num_seqs * num_kv_heads * ceil(group/16) <= 4096): num_waves waves split
  * the batch's flattened 16-token steps evenly, crossing sequence borders
  * (in groups of up to four waves of one workgroup that take the same steps of
- * adjacent kv heads); each writes one partial per (sequence, kv head) it
+ * adjacent kv heads; at exactly two or three workgroups of four waves per
+ * compute unit the earlier-dispatched workgroups take 10-25 % more steps
+ * each, as the hardware runs their waves ahead of the later ones on the same
+ * SIMD); each writes one partial per (sequence, kv head) it
  * touches and a second kernel merges them with the same log-sum-exp rule as
  * the split-K reduce.
  * Same result as clv_paged_decode. num_waves <= 0 picks the device default

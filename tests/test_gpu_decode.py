@@ -78,17 +78,18 @@ def test_balanced_decode_wave_counts(num_waves, dtype):
 
 
 @pytest.mark.parametrize("ctx", [
-    [0, 3000, 17, 811, 0, 4096, 256, 1500, 33, 2222] * 4,  # both pieces long
-    [480] * 10,     # 340 steps: the first piece held at one step per group
+    [0, 3000, 17, 811, 0, 4096, 256, 1500, 33, 2222] * 4,  # every piece long
+    [480] * 10,     # 340 steps: pieces held at one step per group
     [200] * 10,     # 170 steps: fewer than the first piece's groups, even split
 ], ids=["ragged", "clamped", "even"])
+@pytest.mark.parametrize("slots", [2, 3])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_balanced_decode_two_workgroups_per_cu(ctx, dtype):
-    """At two workgroups per compute unit the balanced decode splits the
-    steps in two pieces (the first-dispatched workgroups take the larger
-    one); the merge must find every segment's partials under that split."""
-    waves = 2 * kernels._native.load().clv_default_num_waves()
-    print(f"balanced two-slot waves={waves} dtype={dtype} nseq={len(ctx)}", flush=True)
+def test_balanced_decode_workgroups_per_cu(ctx, slots, dtype):
+    """At two or three workgroups per compute unit the balanced decode splits
+    the steps in one piece per dispatch slot (the older slots take more);
+    the merge must find every segment's partials under that split."""
+    waves = slots * kernels._native.load().clv_default_num_waves()
+    print(f"balanced slots={slots} waves={waves} dtype={dtype} nseq={len(ctx)}", flush=True)
     q, k, v, tables, scale = case(len(ctx) + 5, ctx, 28, 4, 128, 16, dtype)
     got = run_decode(q, k, v, tables, ctx, scale, partition_size=None, num_waves=waves)
     ref = oa.paged_decode(q, k, v, tables, ctx, scale)

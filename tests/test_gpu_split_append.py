@@ -158,15 +158,16 @@ def test_mapped_device_address_and_direct_results():
     assert_attention_close(host, ref, what="merge into pinned host memory")
 
 
-def test_split_append_two_workgroups_per_cu():
-    """The split step at two workgroups per compute unit, where the balanced
-    decode splits its steps in two pieces: the merge with the new token must
-    find every segment's partials under that split (against the fused step
-    at the same wave count and the oracle)."""
+@pytest.mark.parametrize("slots", [2, 3])
+def test_split_append_workgroups_per_cu(slots):
+    """The split step at two or three workgroups per compute unit, where the
+    balanced decode splits its steps in one piece per dispatch slot: the
+    merge with the new token must find every segment's partials under that
+    split (against the fused step at the same wave count and the oracle)."""
     hq, hkv, d, bs, dtype = 28, 4, 128, 16, torch.bfloat16
     ctx = [3000, 17, 811, 0, 4096, 256, 1500, 33] * 3
-    waves = 2 * kernels._native.load().clv_default_num_waves()
-    print(f"split append two-slot waves={waves}", flush=True)
+    waves = slots * kernels._native.load().clv_default_num_waves()
+    print(f"split append slots={slots} waves={waves}", flush=True)
     k, v, tables = make_paged_kv(31, [c + 1 for c in ctx], hkv, d, bs, dtype)
     ks, vs = k.to(DEV), v.to(DEV)
     kf, vf = k.clone().to(DEV), v.clone().to(DEV)
@@ -192,8 +193,8 @@ def test_split_append_two_workgroups_per_cu():
     torch.cuda.synchronize()
     assert _same_bits(ks, kf) and _same_bits(vs, vf)
     ref = oa.paged_decode(q.cpu(), ks.cpu(), vs.cpu(), tables, new, scale)
-    assert_attention_close(out_s.cpu(), ref, what="split, two slots")
-    assert_attention_close(out_f.cpu(), ref, what="fused, two slots")
+    assert_attention_close(out_s.cpu(), ref, what=f"split, {slots} slots")
+    assert_attention_close(out_f.cpu(), ref, what=f"fused, {slots} slots")
 
 
 def test_split_append_workspace_taken_in_between():

@@ -128,6 +128,7 @@ class GpuAttentionBackend:
         self._stage: Dict[str, torch.Tensor] = {}  # pinned host staging buffers, grow-only
         self._stage_np: Dict[str, np.ndarray] = {}  # their bytes as numpy arrays
         self._split_ok: Dict[tuple, bool] = {}  # batch shapes the split decode covers
+        self._offsets: Dict[tuple, tuple] = {}  # staging-buffer offsets per batch shape
         self._stage_done: Optional[torch.cuda.Event] = None  # copies out of them issued
         # Device twin of the staging buffer, reused by every wave: a wave
         # whose results stay on the device returns while its kernels may still
@@ -363,8 +364,9 @@ class GpuAttentionBackend:
             if host is not None and type(items) is list and type(requests) is dict:
                 parsed = host.parse_batch(items, requests)
                 if parsed is not None:
-                    layer, scale, reqs, rows, qs, ks, vs = parsed
-                    return self._run_wave(qs, ks, vs, reqs, int(layer), float(scale), rows=rows)
+                    layer, scale, reqs, rows, first, qs, ks, vs = parsed
+                    return self._run_wave(qs, ks, vs, reqs, int(layer), float(scale), rows=rows,
+                                          rows_first=first)
             layers = set(map(_get_layer, items))
             scales = set(map(_get_scale, items))
             if len(layers) == 1 and len(scales) == 1:
@@ -494,9 +496,12 @@ class GpuAttentionBackend:
         return None
 
     def _run_wave(self, qs, ks, vs, reqs: List[_Request], layer: int, score_scale: float,
-                  packed: bool = False, rows: Optional[np.ndarray] = None):
+                  packed: bool = False, rows: Optional[np.ndarray] = None,
+                  rows_first: Optional[int] = None):
         """One append + decode over distinct requests. qs / ks / vs: lists of
         per-request payloads, or stacked tensors (packed; returns one tensor).
+        rows / rows_first: the requests' table rows and, when known, whether
+        they run consecutively from rows_first (-1: they do not).
 
         Payloads are validated and staged before any request state changes:
         a malformed call raises and leaves every request as it was (the
@@ -526,13 +531,17 @@ class GpuAttentionBackend:
         # the batch shape, so their device views are built once per shape.
         # q and the lengths lead, so that the split decode below can upload
         # them and start before k, v and the bookkeeping are done.
-        qb = n * hq * d * torch.finfo(dt).bits // 8
-        kb = n * hkv * d * torch.finfo(kdt).bits // 8
-        o_i = _align(qb)
-        o_k = o_i + _align(8 * n)
-        o_v = o_k + _align(kb)
-        o_w = o_v + _align(kb)
-        o_u = o_w + 8 * n
+        okey = (n, hq, hkv, d, dt, kdt)
+        offs = self._offsets.get(okey)
+        if offs is None:
+            qb = n * hq * d * dt.itemsize
+            kb = n * hkv * d * kdt.itemsize
+            o_i = _align(qb)
+            o_k = o_i + _align(8 * n)
+            o_v = o_k + _align(kb)
+            o_w = o_v + _align(kb)
+            offs = self._offsets[okey] = (qb, kb, o_i, o_k, o_v, o_w, o_w + 8 * n)
+        qb, kb, o_i, o_k, o_v, o_w, o_u = offs
         nu_max = self.tables.pending_count() + n
         buf = self._staging("wave", (o_u + 12 * nu_max,), torch.uint8)
         bnp = self._stage_np["wave"]
@@ -617,7 +626,10 @@ class GpuAttentionBackend:
                 ctx_out = torch.empty_like(q)
 
             def table():
-                if rows[-1] - rows[0] == n - 1 and (n < 3 or bool((np.diff(rows) == 1).all())):
+                if rows_first is not None:
+                    if rows_first >= 0:
+                        return self.tables.rows_range(rows_first, n)
+                elif rows[-1] - rows[0] == n - 1 and (n < 3 or bool((np.diff(rows) == 1).all())):
                     return self.tables.rows_range(int(rows[0]), n)
                 return self.tables.rows(rows.tolist(), rows_dev)
 

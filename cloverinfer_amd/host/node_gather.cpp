@@ -81,8 +81,9 @@ PyObject *key(const char *name) {
 // One pass over a decode batch (a list of item dicts) for the backend's
 // common case: every item of one layer and one score scale (compared as the
 // backend's sets compare them), each naming a distinct known request.
-// Returns (layer, scale, requests, rows, queries, keys, values) with rows an
-// int64 array of the requests' table rows, or None whenever the batch is not
+// Returns (layer, scale, requests, rows, first, queries, keys, values) with
+// rows an int64 array of the requests' table rows and first the row they run
+// consecutively from (-1 when they do not), or None whenever the batch is not
 // that case (an item that is no dict or lacks a field, an unknown request
 // id, two items of one request, mixed layers or scales): the backend's
 // general path then takes it and raises its own errors. Errors raised by the
@@ -134,10 +135,15 @@ py::object parse_batch(py::list items, py::dict requests) {
     PyList_SET_ITEM(ks.ptr(), i, (Py_INCREF(k), k));
     PyList_SET_ITEM(vs.ptr(), i, (Py_INCREF(v), v));
   }
-  std::vector<int64_t> sorted(r, r + n);
-  std::sort(sorted.begin(), sorted.end());
-  if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) return py::none();
-  return py::make_tuple(layer0, scale0, reqs, rows, qs, ks, vs);
+  bool consecutive = true;
+  for (Py_ssize_t i = 1; i < n && consecutive; ++i) consecutive = r[i] == r[0] + i;
+  if (!consecutive) {  // consecutive rows are distinct; others are checked
+    std::vector<int64_t> sorted(r, r + n);
+    std::sort(sorted.begin(), sorted.end());
+    if (std::adjacent_find(sorted.begin(), sorted.end()) != sorted.end()) return py::none();
+  }
+  return py::make_tuple(layer0, scale0, reqs, rows, consecutive ? r[0] : (int64_t)-1, qs, ks,
+                        vs);
 }
 
 }  // namespace

@@ -87,10 +87,21 @@ def test_parse_batch_uniform_and_refusals(gather):
         return out
 
     it = items()
-    layer, scale, rq, rows, qs, ks, vs = gather.parse_batch(it, reqs)
+    layer, scale, rq, rows, first, qs, ks, vs = gather.parse_batch(it, reqs)
     assert (layer, scale) == (1, 0.25)
     assert rq == [reqs[x["request_id"]] for x in it]
     assert rows.dtype == np.int64 and rows.tolist() == [r.row for r in rq]
+    assert first == -1                                    # rows 7, 10, 13, ...: not consecutive
+    seq = {f"s{i}": _Req(40 + i) for i in range(5)}
+    run = [{"request_id": f"s{i}", "layer_idx": 0, "query": torch.randn(2, 4),
+            "key": torch.randn(1, 4), "value": torch.randn(1, 4)} for i in range(5)]
+    assert gather.parse_batch(run, seq)[4] == 40          # rows 40..44 in order
+    assert gather.parse_batch(run[::-1], seq)[4] == -1    # the same rows, descending
+    swap = [run[1], run[0]] + run[2:]
+    assert gather.parse_batch(swap, seq)[4] == -1
+    assert gather.parse_batch(run[:1], seq)[4] == 40      # one request
+    dup = [run[0], run[0]]
+    assert gather.parse_batch(dup, seq) is None           # repeated request, rows 40, 40
     assert all(a is x["query"] and b is x["key"] and c is x["value"]
                for a, b, c, x in zip(qs, ks, vs, it))
     nos = [{k: v for k, v in x.items() if k != "score_scale"} for x in it]

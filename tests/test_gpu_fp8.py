@@ -91,6 +91,34 @@ def test_fp8_decode_matches_oracle(hq, hkv, bs, qdt):
     assert torch.equal(out[4].float().cpu(), torch.zeros(hq, d))
 
 
+@pytest.mark.parametrize("slots", [2, 3])
+def test_fp8_decode_workgroups_per_cu(slots):
+    """fp8 pools at two (the default) and three workgroups per compute unit,
+    with enough steps that the balanced split comes in one piece per
+    dispatch slot (ragged contexts, about 2,000 steps over 512 or 768
+    four-wave groups)."""
+    hq, hkv, d, bs, qdt = 28, 4, 128, 16, torch.bfloat16
+    ctx = [int(c) for c in torch.randint(0, 4097, (20,),
+                                          generator=torch.Generator().manual_seed(slots))]
+    ctx[3], ctx[7] = 0, 1
+    ks = torch.linspace(0.05, 3.0, hkv)
+    vs = torch.linspace(2.0, 0.1, hkv)
+    waves = slots * kernels._native.load().clv_default_num_waves()
+    print(f"fp8 decode slots={slots} waves={waves}", flush=True)
+    kc, vc, tables = _fp8_pools(100 + slots, ctx, hkv, d, bs, ks, vs)
+    q = torch.randn(len(ctx), hq, d, generator=torch.Generator().manual_seed(19)).to(qdt)
+    out = torch.empty(q.shape, dtype=qdt, device=DEV)
+    scale = 1.0 / math.sqrt(d)
+    kernels.paged_attention(out, q.to(DEV), kc.to(DEV), vc.to(DEV), padded_tables(tables).to(DEV),
+                            torch.tensor(ctx, dtype=torch.int32, device=DEV), bs, max(ctx),
+                            scale=scale, num_waves=waves, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    kf = kc.float() * ks.view(1, 1, -1, 1)
+    vf = vc.float() * vs.view(1, 1, -1, 1)
+    ref = oa.paged_decode(q, kf, vf, tables, ctx, scale)
+    assert_attention_close(out.cpu(), ref, what=f"fp8, {slots} slots")
+
+
 def test_fp8_backend_steps():
     """kv_dtype="fp8" with a per-head kv_scale: fp32 and bf16 payloads, three
     decode steps on two layers, against the restated CpuAttentionBackend fed

@@ -167,23 +167,27 @@ __device__ __forceinline__ void valu_attend(const T *q0, int64_t q_stride_head, 
       kf[v] = to_f32(ke[v]);
       vf[v] = to_f32(ve[v]);
     }
+    // Rows g >= ng are skipped by a guard, not a break: a loop with one exit
+    // and a constant trip count unrolls, which keeps the per-row arrays in
+    // registers.
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-      if (g >= ng) break;
-      float sc = 0.f;
+      if (g < ng) {
+        float sc = 0.f;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) sc += qf[g][v] * kf[v];
+        for (int v = 0; v < VEC; ++v) sc += qf[g][v] * kf[v];
 #pragma unroll
-      for (int o2 = 1; o2 < LPT; o2 <<= 1) sc += shfl_xor(sc, o2);
-      const float x = ok ? sc * scale_log2 : kNegInf;
-      const float m_new = fmaxf(m[g], x);
-      const float msub = (m_new == kNegInf) ? 0.f : m_new;
-      const float a = fast_exp2(m[g] - msub);
-      const float pr = fast_exp2(x - msub);
-      l[g] = l[g] * a + pr;
+        for (int o2 = 1; o2 < LPT; o2 <<= 1) sc += shfl_xor(sc, o2);
+        const float x = ok ? sc * scale_log2 : kNegInf;
+        const float m_new = fmaxf(m[g], x);
+        const float msub = (m_new == kNegInf) ? 0.f : m_new;
+        const float a = fast_exp2(m[g] - msub);
+        const float pr = fast_exp2(x - msub);
+        l[g] = l[g] * a + pr;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[g][v] = acc[g][v] * a + pr * vf[v];
-      m[g] = m_new;
+        for (int v = 0; v < VEC; ++v) acc[g][v] = acc[g][v] * a + pr * vf[v];
+        m[g] = m_new;
+      }
     }
   }
 
@@ -192,20 +196,21 @@ __device__ __forceinline__ void valu_attend(const T *q0, int64_t q_stride_head, 
   for (int off = LPT; off < 64; off <<= 1) {
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-      if (g >= ng) break;
-      const float m2 = shfl_xor(m[g], off);
-      const float l2 = shfl_xor(l[g], off);
-      const float M = fmaxf(m[g], m2);
-      const float Msub = (M == kNegInf) ? 0.f : M;
-      const float a1 = fast_exp2(m[g] - Msub);
-      const float a2 = fast_exp2(m2 - Msub);
-      l[g] = l[g] * a1 + l2 * a2;
+      if (g < ng) {
+        const float m2 = shfl_xor(m[g], off);
+        const float l2 = shfl_xor(l[g], off);
+        const float M = fmaxf(m[g], m2);
+        const float Msub = (M == kNegInf) ? 0.f : M;
+        const float a1 = fast_exp2(m[g] - Msub);
+        const float a2 = fast_exp2(m2 - Msub);
+        l[g] = l[g] * a1 + l2 * a2;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const float o2 = shfl_xor(acc[g][v], off);
-        acc[g][v] = acc[g][v] * a1 + o2 * a2;
+        for (int v = 0; v < VEC; ++v) {
+          const float o2 = shfl_xor(acc[g][v], off);
+          acc[g][v] = acc[g][v] * a1 + o2 * a2;
+        }
+        m[g] = M;
       }
-      m[g] = M;
     }
   }
   if (row == 0) {

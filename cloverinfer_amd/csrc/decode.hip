@@ -30,8 +30,6 @@
 namespace clv {
 namespace {
 
-constexpr int kStep = 32;  // tokens per wave step in the MFMA kernel
-
 template <typename T>
 __device__ __forceinline__ KvView kv_view(const DecodeParams &p, int s, int kvh) {
   KvView v;

@@ -39,7 +39,10 @@ def case(seed, ctx, hq, hkv, d, bs, dtype, scale=None, value_scale=1.0):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("hq,hkv,d", [(8, 8, 128), (28, 4, 128), (32, 8, 64), (16, 1, 128),
                                       (32, 1, 64), (6, 2, 256), (4, 4, 32), (128, 4, 128),
-                                      (96, 8, 64), (24, 12, 128)])
+                                      (96, 8, 64), (24, 12, 128),
+                                      # VALU head dims with more than four query heads per
+                                      # kv head (the kernel's 16-row query-head chunk)
+                                      (16, 2, 256), (28, 4, 32)])
 @pytest.mark.parametrize("partition", [None, 0, 32, 512])
 def test_decode_matches_oracle(dtype, hq, hkv, d, partition):
     ctx = [1, 17, 31, 32, 33, 100, 511, 513, 1000, 0]

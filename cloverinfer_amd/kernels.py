@@ -269,7 +269,7 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
         num_waves = num_waves or lib.clv_default_num_waves_fp8()
         nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
                                                   a.head_dim, num_waves)
-        ws = splitk_workspace(dev, nbytes)
+        ws = splitk_workspace(dev, nbytes, stream)
         _native.check(lib.clv_paged_decode_fp8(a, ks.data_ptr(), vs.data_ptr(), num_waves,
                                                ws.data_ptr(), ws.numel(), stream),
                       "clv_paged_decode_fp8")
@@ -282,14 +282,14 @@ def paged_attention(out: torch.Tensor, q: torch.Tensor, k_cache: torch.Tensor,
         if mode == "balanced":
             nbytes = lib.clv_balanced_workspace_bytes(a.num_seqs, a.num_heads, a.num_kv_heads,
                                                       a.head_dim, num_waves)
-            ws = splitk_workspace(dev, nbytes)
+            ws = splitk_workspace(dev, nbytes, stream)
             _native.check(lib.clv_paged_decode_balanced(a, num_waves, ws.data_ptr(), ws.numel(),
                                                         stream), "clv_paged_decode_balanced")
             return
     if partition_size == 0 or a.max_context_len <= partition_size:
         _native.check(lib.clv_paged_decode(a, stream), "clv_paged_decode")
         return
-    ws = splitk_workspace(dev, workspace_bytes(a, partition_size))
+    ws = splitk_workspace(dev, workspace_bytes(a, partition_size), stream)
     _native.check(
         lib.clv_paged_decode_splitk(a, partition_size, ws.data_ptr(), ws.numel(), stream),
         "clv_paged_decode_splitk",
@@ -375,7 +375,8 @@ class AppendDecodeLaunch:
 
     def bind(self):
         """A callable that reissues this launch, as it stands now, on the
-        current stream with no further Python work beyond the C call (for a
+        stream that is current when bind() is called (and that stream's
+        workspace), with no further Python work beyond the C call (for a
         caller that replays one step over fixed buffers); it returns the C
         status code. The callable holds a copy of the argument block and
         the tensors it points into that the launch owns (the new rows if

@@ -99,6 +99,22 @@ def test_balanced_decode_workgroups_per_cu(ctx, slots, dtype):
     assert_attention_close(got, ref, what=f"balanced W={waves}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (8, 1), (32, 32)])  # head groups 2, 1, 2
+@pytest.mark.parametrize("slots", [2, 3])
+def test_balanced_decode_workgroups_per_cu_head_groups(hq, hkv, slots):
+    """The per-slot split with head groups of two and one (the pieces hold
+    4 * CUs / head_group groups each) on a ragged batch long enough for every
+    piece."""
+    waves = slots * kernels._native.load().clv_default_num_waves()
+    ctx = [int(c) for c in torch.randint(0, 3000, (24,),
+                                          generator=torch.Generator().manual_seed(hkv + slots))]
+    print(f"balanced slots={slots} hq={hq} hkv={hkv} waves={waves}", flush=True)
+    q, k, v, tables, scale = case(hkv * 10 + slots, ctx, hq, hkv, 128, 16, torch.bfloat16)
+    got = run_decode(q, k, v, tables, ctx, scale, partition_size=None, num_waves=waves)
+    ref = oa.paged_decode(q, k, v, tables, ctx, scale)
+    assert_attention_close(got, ref, what=f"balanced {hq}/{hkv} W={waves}")
+
+
 @pytest.mark.parametrize("d,bs", [(128, 16), (64, 16), (128, 8), (64, 4)])
 def test_fp32_balanced_decode_is_fp32_exact(d, bs):
     """fp32 pools on the fp32 MFMA wave: nothing is rounded below fp32, so

@@ -528,7 +528,7 @@ def measure_decode(args, name):
     out_host = out.cpu()
     log(f"{name}: step {ms:.4f} ms, " + ", ".join(f"{n} {e[0]:.1f} us" for n, e in zip(names, ev)))
     step_bytes = w["algo_bytes"] + append_bytes
-    kernel = {"balanced": "paged_decode_stream", "split": "paged_decode_mfma (split-K partials)",
+    kernel = {"balanced": "paged_decode_stream", "split": "paged_decode_stream (split-K partials)",
               "single": "paged_decode_mfma (single pass)"}[mode]
     kernel_bytes = w["algo_bytes"]
     if fused is not None:

@@ -387,26 +387,28 @@ struct DecodeWave {
   }
 
   // After reduce_rowsum(): write this wave's normalised partial of rows
-  // g < ng as rows (slot0 + g) of the workspace: context, row max (natural
-  // log domain) and row sum.
+  // g < ng as rows (row0 + g * rstride) of the workspace: context, row max
+  // (natural log domain) and row sum.
   __device__ __forceinline__ void store_partial(float *ws_o, float *ws_m, float *ws_l,
-                                                int64_t row0, int ng) const {
+                                                int64_t row0, int ng,
+                                                int64_t rstride = 1) const {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int g = 4 * j + r;
       const float l = shfl(l_run, g);
       const float mrow = shfl(m_run, g);
       if (g >= ng) continue;
+      const int64_t row = row0 + g * rstride;
       const float inv = (l > 0.f ? 1.f / l : 0.f) * (KV8 ? vscale : 1.f);
-      float *dst = ws_o + (row0 + g) * D + n16 * CH;
+      float *dst = ws_o + row * D + n16 * CH;
 #pragma unroll
       for (int m = 0; m < CH; m += 4) {
         const f32x4 v = {o[m][r] * inv, o[m + 1][r] * inv, o[m + 2][r] * inv, o[m + 3][r] * inv};
         store_vec<f32x4>(dst + m, v);
       }
       if (n16 == 0) {
-        ws_m[row0 + g] = l > 0.f ? mrow * kLn2 : kNegInf;
-        ws_l[row0 + g] = l;
+        ws_m[row] = l > 0.f ? mrow * kLn2 : kNegInf;
+        ws_l[row] = l;
       }
     }
   }
@@ -613,23 +615,25 @@ struct DecodeWaveF32 {
 
   // As DecodeWave::store_partial, with this wave's output columns.
   __device__ __forceinline__ void store_partial(float *ws_o, float *ws_m, float *ws_l,
-                                                int64_t row0, int ng) const {
+                                                int64_t row0, int ng,
+                                                int64_t rstride = 1) const {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int g = 4 * j + r;
       const float l = shfl(l_run, g);
       const float mrow = shfl(m_run, g);
       if (g >= ng) continue;
+      const int64_t row = row0 + g * rstride;
       const float inv = l > 0.f ? 1.f / l : 0.f;
-      float *dst = ws_o + (row0 + g) * D + 4 * n16;
+      float *dst = ws_o + row * D + 4 * n16;
 #pragma unroll
       for (int m = 0; m < CH; m += 4) {
         const f32x4 v = {o[m][r] * inv, o[m + 1][r] * inv, o[m + 2][r] * inv, o[m + 3][r] * inv};
         store_vec<f32x4>(dst + 16 * m, v);
       }
       if (n16 == 0) {
-        ws_m[row0 + g] = l > 0.f ? mrow * kLn2 : kNegInf;
-        ws_l[row0 + g] = l;
+        ws_m[row] = l > 0.f ? mrow * kLn2 : kNegInf;
+        ws_l[row] = l;
       }
     }
   }

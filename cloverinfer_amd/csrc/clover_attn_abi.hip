@@ -712,6 +712,7 @@ int clv_chunked_prefill(const clv_prefill_args *a, clv_stream_t stream) {
   p.max_query_len = a->max_query_len;
   p.num_blocks = a->num_blocks;
   p.scale_log2 = a->scale * 1.4426950408889634f;
+  p.cus_per_xcd = device_compute_units() / 8;
   const DType dt = (DType)a->dtype;
   hipError_t err;
   if (clv::prefill_mfma_supported(dt, a->head_dim, a->block_size))

@@ -99,6 +99,9 @@ struct PrefillParams {
   int32_t num_seqs, num_tokens, num_heads, num_kv_heads, head_dim;
   int32_t group, block_shift, max_blocks_per_seq, max_query_len, num_blocks;
   float scale_log2;
+  // Compute units per XCD (the device's count / 8), for the prefill's
+  // dispatch order; 0 keeps the natural order.
+  int32_t cus_per_xcd;
 };
 
 enum class DType : int { F32 = 0, F16 = 1, BF16 = 2 };

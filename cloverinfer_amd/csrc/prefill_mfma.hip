@@ -85,6 +85,29 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
 }
 
+// Work item of dispatch position i within one XCD. A workgroup holds most of
+// a compute unit's LDS, so the XCD's workgroups run in rounds of one per CU
+// (`cus` of them), in dispatch order. The items of one (sequence, kv head)
+// are its n_q query tiles, consecutive and heaviest first (a later tile
+// attends to more keys). The first round takes the items in that natural
+// order: the query tiles of one kv head run side by side and share their K/V
+// reads in the XCD's L2. Each later round holds the same items as in the
+// natural order but dispatches them by weight, heaviest tile of every kv head
+// first, so that the CUs that finish first (those given the lightest tiles)
+// take the heaviest ones. Of the XCD's per_xcd positions, `valid` hold items;
+// when a round does not hold whole kv heads the natural order is kept.
+__host__ __device__ inline int dispatch_slot(int i, int per_xcd, int valid, int n_q, int cus) {
+  if (valid > per_xcd) valid = per_xcd;
+  if (cus <= 0 || n_q <= 1 || cus % n_q != 0 || per_xcd % n_q != 0 || i < cus || i >= valid)
+    return i;
+  const int r0 = i / cus * cus;
+  const int len = valid - r0 < cus ? valid - r0 : cus;
+  if (len % n_q != 0) return i;
+  const int heads = len / n_q;
+  const int u = i - r0;
+  return r0 + (u % heads) * n_q + u / heads;
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(kThreads)
 chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
@@ -112,9 +135,12 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
   __shared__ int sOvf;  // set when a bf16 V value did not fit fp16
 
   // XCD-aware remap: consecutive ids go round-robin over the 8 XCDs; give
-  // each XCD a contiguous range of logical work items.
+  // each XCD a contiguous range of logical work items, in the order
+  // dispatch_slot sets.
   const int per_xcd = gridDim.x / 8;
-  const int L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int xcd0 = (blockIdx.x % 8) * per_xcd;
+  const int L = xcd0 + dispatch_slot(blockIdx.x / 8, per_xcd, total - xcd0, n_qtiles,
+                                     p.cus_per_xcd);
   if (L >= total) return;
   const int qt = n_qtiles - 1 - L % n_qtiles;  // longest query tiles first
   const int rest = L / n_qtiles;

@@ -62,8 +62,15 @@ struct StreamSplit {
   int64_t W, N, Gp;
   int S;
   int64_t b1, b2, b3;  // first steps of pieces 1..3 (N past the last piece)
+  // Every product in start() and owner() is a group count (<= W) times a
+  // step count (<= N). When W * N fits 32 bits they run in 32-bit unsigned
+  // arithmetic, with the same results: a 64-bit division is a long
+  // instruction sequence on the GPU, and these sit on every wave's way to
+  // its first load and on the merge's way to its partials.
+  bool narrow;
   __host__ __device__ StreamSplit(const DecodeParams &p, int64_t W_, int64_t N_)
-      : W(W_), N(N_), Gp(p.slot_groups), S(1), b1(N_), b2(N_), b3(N_) {
+      : W(W_), N(N_), Gp(p.slot_groups), S(1), b1(N_), b2(N_), b3(N_),
+        narrow((uint64_t)W_ * (uint64_t)N_ <= 0xffffffffull) {
     if (p.slot_count > 1 && Gp > 0 && Gp < W) {
       S = (int)min((int64_t)min(p.slot_count, kMaxSlots), (W + Gp - 1) / Gp);
       const int64_t w0 = groups(0) * p.slot_q8[0], w1 = groups(1) * p.slot_q8[1];
@@ -88,21 +95,27 @@ struct StreamSplit {
   __host__ __device__ __forceinline__ int64_t base(int k) const {
     return k <= 0 ? 0 : k == 1 ? b1 : k == 2 ? b2 : k == 3 ? b3 : N;
   }
+  // floor((a * b - sub) / c) for 0 <= a <= N, 0 <= b <= W (or the other
+  // way round), sub in {0, 1} with a * b >= sub, c > 0.
+  __host__ __device__ __forceinline__ int64_t muldiv(int64_t a, int64_t b, int sub,
+                                                     int64_t c) const {
+    if (narrow) return (int64_t)(((uint32_t)a * (uint32_t)b - (uint32_t)sub) / (uint32_t)c);
+    return (a * b - sub) / c;
+  }
   // First step of group w (w <= W; start(W) = N).
   __host__ __device__ __forceinline__ int start(int w) const {
-    if (S == 1) return (int)((int64_t)w * N / W);
+    if (S == 1) return (int)muldiv(w, N, 0, W);
     if (w >= W) return (int)N;
     const int k = (int)min((int64_t)w / Gp, (int64_t)S - 1);
     const int64_t lo = base(k);
-    return (int)(lo + (w - (int64_t)k * Gp) * (base(k + 1) - lo) / groups(k));
+    return (int)(lo + muldiv(w - (int64_t)k * Gp, base(k + 1) - lo, 0, groups(k)));
   }
   // Group owning step x (0 <= x < N): the largest w with start(w) <= x.
   __host__ __device__ __forceinline__ int owner(int x) const {
-    if (S == 1) return (int)(((int64_t)(x + 1) * W - 1) / N);
+    if (S == 1) return (int)muldiv(x + 1, W, 1, N);
     const int k = (S > 3 && b3 <= x) ? 3 : (S > 2 && b2 <= x) ? 2 : b1 <= x ? 1 : 0;
     const int64_t lo = base(k);
-    return (int)((int64_t)k * Gp +
-                 ((int64_t)(x - lo + 1) * groups(k) - 1) / (base(k + 1) - lo));
+    return (int)((int64_t)k * Gp + muldiv(x - lo + 1, groups(k), 1, base(k + 1) - lo));
   }
 };
 
@@ -201,13 +214,22 @@ paged_decode_stream(const DecodeParams p, const int32_t *__restrict__ tables,
   const int en = uni(split.start(wid + 1));
   if (st >= en) return;
 
-  // Segment holding step st: the last one whose first step is <= st.
+  // Segment holding step st: the last one whose first step is <= st. The
+  // first steps never decrease and s_seg[0] = 0 <= st, so those segments
+  // are a prefix: each round the lanes test 64 evenly spaced candidates at
+  // once and the highest passing lane narrows the range (two rounds cover
+  // 4096 segments, against twelve dependent LDS reads of a binary search).
   int seg;
   {
-    int lo = 0, hi = nseg - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_seg[mid] <= st) lo = mid; else hi = mid - 1;
+    const int lane = threadIdx.x & 63;
+    int lo = 0, n = nseg;  // the answer lies in [lo, lo + n); s_seg[lo] <= st
+    while (n > 1) {
+      const int stride = (n + 63) / 64;
+      const bool le = lane * stride < n && s_seg[lo + lane * stride] <= st;
+      const uint64_t m = __ballot(le);  // bit 0 is set (s_seg[lo] <= st)
+      const int k = 63 - __builtin_clzll(m);
+      lo += k * stride;
+      n = min(stride, n - k * stride);
     }
     seg = uni(lo);
   }
@@ -425,8 +447,20 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
   const int kvg = kvh / HG, wk = kvh - kvg * HG;
   const int seg = (s * (p.num_kv_heads / HG) + kvg) * p.n_gchunks + gall / 16;
   const int g = gall % 16;
-  const int a = p.seg_prefix[seg] + p.stream_run_cost, b = p.seg_prefix[seg + 1];
-  const int64_t N = p.seg_prefix[p.num_segments];
+  // The segment bounds and the step total are wave-uniform and read-only
+  // here: three scalar loads issued together, one wait (the split's
+  // arithmetic then runs on the scalar unit).
+  int a, b, n_total;
+  {
+    const int32_t *ps = p.seg_prefix + __builtin_amdgcn_readfirstlane(seg);
+    const int32_t *pn = p.seg_prefix + p.num_segments;
+    uint64_t ab;
+    asm volatile("s_load_dwordx2 %0, %2, 0x0\n\ts_load_dword %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(ab), "=s"(n_total) : "s"(ps), "s"(pn) : "memory");
+    a = (int)(uint32_t)ab + p.stream_run_cost;
+    b = (int)(uint32_t)(ab >> 32);
+  }
+  const int64_t N = n_total;
   const int64_t W = min((int64_t)(p.num_waves / HG), N);
   int n = 0, w0 = 0;
   if (b > a) {

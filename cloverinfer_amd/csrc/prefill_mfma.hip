@@ -471,7 +471,11 @@ chunked_prefill_mfma(const PrefillParams p, int bq, int n_qtiles, int total) {
       return __all(sValid[tile % 3][lane] != 0) && tile * kBK + kBK - 1 <= wave_lim;
     };
 
-    if (tid == 0) sOvf = 0;
+    // Cleared by the fast pass only: every wave reads the flag after the fast
+    // pass's last barrier, so a clear at the start of the exact pass could
+    // race a slower wave's read, and waves that disagreed on running the
+    // exact pass would wait at different barriers.
+    if (!EXACT && tid == 0) sOvf = 0;
     fetch_blocks(0);
     if (ntiles > 0) {
       load_tile(0);

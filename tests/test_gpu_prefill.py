@@ -148,6 +148,24 @@ def test_prefill_bf16_values_beyond_fp16_range():
     assert_attention_close(got, ref, what="prefill bf16 beyond fp16 range")
 
 
+def test_prefill_every_workgroup_takes_the_exact_pass():
+    """Every workgroup meets a bf16 V value beyond fp16's range in its first
+    tile (token 0 of every sequence and kv head, which every query row sees)
+    and reruns its rows in the exact pass, all at once. The overflow flag is
+    read by every wave after the fast pass; the exact pass must not clear it
+    while another wave may still be reading it (waves that disagreed on taking
+    the exact pass would wait at different barriers)."""
+    cached, new = [512, 700, 256, 1000], [512, 300, 700, 128]
+    q, k, v, tables, ctx, qsl = build(91, cached, new, 32, 8, 128, 16, torch.bfloat16)
+    for s in range(len(cached)):
+        v[tables[s][0], 0, :, 3] = 2.0e5
+    scale = 1.0 / math.sqrt(128)
+    got = run_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert torch.isfinite(got.float()).all()
+    ref = oracle_prefill(q, k, v, tables, ctx, qsl, scale)
+    assert_attention_close(got, ref, what="prefill, exact pass in every workgroup")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])  # MFMA and VALU kernels
 def test_prefill_max_query_len_none_and_too_small(dtype):
     """max_query_len=None is computed from query_start_loc; a value below the

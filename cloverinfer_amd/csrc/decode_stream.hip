@@ -455,8 +455,10 @@ __global__ void __launch_bounds__(256) stream_reduce(const DecodeParams p) {
     const int32_t *ps = p.seg_prefix + __builtin_amdgcn_readfirstlane(seg);
     const int32_t *pn = p.seg_prefix + p.num_segments;
     uint64_t ab;
+    // Early-clobber outputs: the first load's destination is written when its
+    // data returns, so it must not share registers with the second's address.
     asm volatile("s_load_dwordx2 %0, %2, 0x0\n\ts_load_dword %1, %3, 0x0\n\ts_waitcnt lgkmcnt(0)"
-                 : "=s"(ab), "=s"(n_total) : "s"(ps), "s"(pn) : "memory");
+                 : "=&s"(ab), "=&s"(n_total) : "s"(ps), "s"(pn) : "memory");
     a = (int)(uint32_t)ab + p.stream_run_cost;
     b = (int)(uint32_t)(ab >> 32);
   }
